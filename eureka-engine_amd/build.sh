@@ -1,0 +1,8 @@
+#!/bin/bash
+# Builds libeureka_moe.so (gfx950) in place. -ffp-contract=off: the exact tier's float ops are
+# executed as written; -packed-fp32-ops off: no v_pk_*_f32.
+set -euo pipefail
+cd "$(dirname "$0")"
+hipcc --offload-arch=gfx950 -O3 -std=c++17 -fPIC -shared -ffp-contract=off \
+  -Xclang -target-feature -Xclang -packed-fp32-ops \
+  -o libeureka_moe.so csrc/llb_moe_hip.cpp csrc/moe_exact.hip csrc/moe_q8.hip csrc/moe_synth.hip "$@"

@@ -1,0 +1,296 @@
+// llb_moe_hip.cpp -- the C ABI (include/llb_moe_hip.h): the backend contract on HIP and the
+// per-layer launch sequence of the MoE FFN.
+#include "../../include/llb_moe_hip.h"
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "moe_kernels.h"
+
+int launch_gauss(uint64_t seed, uint64_t stream, uint64_t i0, uint64_t n, float sigma, float* out, hipStream_t st);
+int launch_gen_rows(uint32_t fm, uint64_t seed, uint64_t stream, uint64_t r0, uint64_t nr, uint32_t cols, float sigma,
+                    uint8_t* out, hipStream_t st);
+int moe_q8_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const float* x1, float* y, const uint32_t* ids,
+                   const float* wt, const float* sgo, uint8_t* scratch, hipStream_t st);
+size_t moe_q8_scratch(const llb_moe_layer* L, uint32_t T);
+int launch_group(const uint32_t* ids, uint32_t n, uint32_t nk, uint32_t ne, uint32_t* off, uint32_t* xmap,
+                 uint32_t* inv, uint32_t* cnt, hipStream_t st);
+int launch_q8_1(const float* x, uint32_t n, int8_t* q, float2* ds, hipStream_t st);
+
+static thread_local char g_err[512];
+static hipStream_t g_stream = nullptr;
+
+static int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+static int hip_ok(hipError_t e, const char* what) {
+  if (e == hipSuccess) return 0;
+  return fail(LLB_HIP_EDEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+// a launch's error (bad configuration, no device) is what hipGetLastError reports right after it
+static int launched(int rc, const char* what) {
+  if (rc != 0) return fail(LLB_HIP_EINVAL, "%s: no kernel for this format / shape", what);
+  return hip_ok(hipGetLastError(), what);
+}
+
+template <class T> static T* dp(llb_dptr p) { return reinterpret_cast<T*>((uintptr_t)p); }
+
+static uint64_t row_bytes(uint32_t fm, uint32_t cols) {
+  switch (fm) {
+    case LLB_FM_F32: return (uint64_t)cols * 4;
+    case LLB_FM_Q8_0: return (uint64_t)cols / 32 * 34;
+    case LLB_FM_Q4_K: return (uint64_t)cols / 256 * 144;
+    case LLB_FM_Q6_K: return (uint64_t)cols / 256 * 210;
+    case LLB_FM_Q5_K: return (uint64_t)cols / 256 * 176;
+  }
+  return 0;
+}
+static bool expert_fm(uint32_t f) {
+  return f == LLB_FM_Q8_0 || f == LLB_FM_Q4_K || f == LLB_FM_Q6_K || f == LLB_FM_Q5_K;
+}
+// llb_cdepth (host/llb_host.c:52-58) and llb_tuned (:64-76) for the formats this path takes
+static uint32_t cdepth(uint32_t cols) {
+  uint32_t d = 0;
+  while ((1u << d) < cols) d++;
+  return d - 2;
+}
+static bool tuned(uint32_t fm, uint32_t cols) {
+  uint32_t d = cdepth(cols), cg = cols / 4;
+  if (fm == LLB_FM_F32) return d >= 9 && d <= 12;
+  if (fm == LLB_FM_Q4_K || fm == LLB_FM_Q6_K) return (cg % 256 == 0 && d >= 8 && d <= 13) || (d >= 9 && d <= 11);
+  if (fm == LLB_FM_Q5_K) return cg % 256 == 0 && d >= 8 && d <= 13;
+  return false;
+}
+
+extern "C" {
+
+const char* llb_hip_last_error(void) { return g_err; }
+
+int llb_hip_init(int device) {
+  g_err[0] = 0;
+  return hip_ok(hipSetDevice(device), "hipSetDevice");
+}
+int llb_hip_set_stream(void* s) {
+  g_stream = (hipStream_t)s;
+  return 0;
+}
+llb_dptr llb_hip_alloc_zero(size_t bytes) {
+  void* p = nullptr;
+  if (hip_ok(hipMalloc(&p, bytes ? bytes : 4), "hipMalloc") != 0) return 0;
+  if (hip_ok(hipMemset(p, 0, bytes ? bytes : 4), "hipMemset") != 0) {
+    (void)hipFree(p);
+    return 0;
+  }
+  return (llb_dptr)(uintptr_t)p;
+}
+int llb_hip_free(llb_dptr p) { return hip_ok(hipFree(dp<void>(p)), "hipFree"); }
+int llb_hip_zero(llb_dptr p, size_t bytes) { return hip_ok(hipMemsetAsync(dp<void>(p), 0, bytes, g_stream), "llb_zero"); }
+int llb_hip_copy(llb_dptr d, llb_dptr s, size_t bytes) {
+  return hip_ok(hipMemcpyAsync(dp<void>(d), dp<void>(s), bytes, hipMemcpyDeviceToDevice, g_stream), "llb_copy");
+}
+int llb_hip_write(llb_dptr d, const void* h, size_t bytes) {
+  int rc = hip_ok(hipMemcpyAsync(dp<void>(d), h, bytes, hipMemcpyHostToDevice, g_stream), "llb_write");
+  return rc ? rc : hip_ok(hipStreamSynchronize(g_stream), "llb_write");
+}
+int llb_hip_read(void* h, llb_dptr p, size_t bytes) {
+  int rc = hip_ok(hipMemcpyAsync(h, dp<void>(p), bytes, hipMemcpyDeviceToHost, g_stream), "llb_read");
+  return rc ? rc : hip_ok(hipStreamSynchronize(g_stream), "llb_read");
+}
+int llb_hip_sync(void) { return hip_ok(hipStreamSynchronize(g_stream), "llb_sync"); }
+int llb_hip_mem_info(size_t* f, size_t* t) { return hip_ok(hipMemGetInfo(f, t), "hipMemGetInfo"); }
+
+// ---------------------------------------------------------------- layer checks and scratch
+
+static int check_layer(const llb_moe_layer* L, int tier) {
+  if (!L) return fail(LLB_HIP_EINVAL, "null layer");
+  const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
+  if (!L->dm || L->dm % 256 || !L->ef || L->ef % 256) return fail(LLB_HIP_EINVAL, "dm and ef must be multiples of 256");
+  if (!L->ne || L->ne > 1024 || !L->nk || L->nk > L->ne || L->nk > 63)
+    return fail(LLB_HIP_EINVAL, "need 1 <= nk <= min(ne, 63), ne <= 1024");
+  if (!expert_fm(fg) || !expert_fm(fu) || !expert_fm(fd)) return fail(LLB_HIP_EINVAL, "expert formats: Q8_0, Q4_K, Q5_K, Q6_K");
+  if (fz && fu != fg) return fail(LLB_HIP_EINVAL, "fused gate+up needs one format");
+  if (tier == LLB_MOE_EXACT && fg != fu) return fail(LLB_HIP_EINVAL, "exact tier: gate and up in one format");
+  if (!L->router || !L->G || !L->D || (!fz && !L->U)) return fail(LLB_HIP_EINVAL, "null weights");
+  const uint32_t d = cdepth(L->dm);
+  if (!tuned(LLB_FM_F32, L->dm) || d > 11) return fail(LLB_HIP_EINVAL, "router: dm in 1025..8192 (the engine tree)");
+  if (L->sf) {
+    if (L->sf % 256 || !L->shgate || !L->SG || !L->SU || !L->SD) return fail(LLB_HIP_EINVAL, "shared expert: sf % 256, weights");
+    if (L->fsg != L->fsu || !tuned(L->fsg, L->dm) || L->fsg == LLB_FM_Q8_0 || !expert_fm(L->fsg))
+      return fail(LLB_HIP_EINVAL, "shared gate/up: one K-quant format on a tuned width");
+    if (tuned(L->fsd, L->sf) || L->fsd == LLB_FM_Q8_0 || !expert_fm(L->fsd))
+      return fail(LLB_HIP_EINVAL, "shared down: a K-quant on llb_gemv_any's order (untuned width)");
+  }
+  if (64 / (L->nk + (L->sf ? 1 : 0)) < 1) return fail(LLB_HIP_EINVAL, "nk too large");
+  return 0;
+}
+
+static size_t al(size_t n) { return (n + 255) & ~(size_t)255; }
+
+struct ExactScratch {
+  size_t lg, gsu, sa, sgo, act, total;
+};
+static ExactScratch exact_layout(const llb_moe_layer* L, uint32_t T) {
+  ExactScratch s;
+  size_t o = 0;
+  s.lg = o; o += al((size_t)T * (L->ne + 1) * 4);
+  s.gsu = o; o += al((size_t)T * 2 * L->sf * 4 + 4);
+  s.sa = o; o += al((size_t)T * L->sf * 4 + 4);
+  s.sgo = o; o += al((size_t)T * 4);
+  s.act = o; o += al((size_t)T * L->nk * L->ef * 4);
+  s.total = o;
+  return s;
+}
+
+size_t llb_moe_hip_scratch_bytes(const llb_moe_layer* L, uint32_t T, int tier) {
+  if (!L || !T) return 0;
+  const size_t a = exact_layout(L, T).total;
+  if (tier == LLB_MOE_Q8) return a + moe_q8_scratch(L, T);
+  return a;
+}
+
+// router + shared gate logit + shared gate / up (the tree rows), then top-k and sa
+static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* ids, float* wt, uint8_t* sc,
+                 const ExactScratch& s) {
+  float* lg = (float*)(sc + s.lg);
+  float* gsu = (float*)(sc + s.gsu);
+  TreeArgs a{};
+  a.cols = L->dm;
+  a.x = h2;
+  a.T = T;
+  a.xstride = L->dm;
+  a.tch = 16;
+  const uint32_t ns = 1u << (cdepth(L->dm) - 9);
+  a.seg[0] = TreeSeg{dp<uint8_t>(L->router), (uint64_t)L->dm * 4, L->ne, lg, L->ne + 1};
+  a.seg[1] = TreeSeg{dp<uint8_t>(L->shgate), (uint64_t)L->dm * 4, L->sf ? 1u : 0u, lg + L->ne, L->ne + 1};
+  a.seg[2] = TreeSeg{dp<uint8_t>(L->SG), row_bytes(L->fsg, L->dm), L->sf, gsu, 2 * L->sf};
+  a.seg[3] = TreeSeg{dp<uint8_t>(L->SU), row_bytes(L->fsu, L->dm), L->sf, gsu + L->sf, 2 * L->sf};
+  int rc;
+  if ((rc = launched(launch_tree_rows(a, 0, LLB_FM_F32, ns, g_stream), "router"))) return rc;
+  if ((rc = launched(launch_tree_rows(a, 1, LLB_FM_F32, ns, g_stream), "shared gate logit"))) return rc;
+  if ((rc = launched(launch_tree_rows(a, 2, L->fsg, ns, g_stream), "shared gate"))) return rc;
+  if ((rc = launched(launch_tree_rows(a, 3, L->fsu, ns, g_stream), "shared up"))) return rc;
+  TopkArgs k{};
+  k.lg = lg;
+  k.lstride = L->ne + 1;
+  k.ne = L->ne;
+  k.nk = L->nk;
+  k.has_sg = L->sf ? 1 : 0;
+  k.sf = L->sf;
+  k.ids = ids;
+  k.wt = wt;
+  k.sgo = (float*)(sc + s.sgo);
+  k.gsu = gsu;
+  k.sa = (float*)(sc + s.sa);
+  return launched(launch_topk(k, T, g_stream), "topk");
+}
+
+int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dptr x1, llb_dptr y, llb_dptr ids,
+                        llb_dptr wt, llb_dptr scratch, size_t scratch_bytes, int tier) {
+  int rc = check_layer(L, tier);
+  if (rc) return rc;
+  if (T == 0) return 0;
+  if (!h2 || !y || !ids || !wt || !scratch) return fail(LLB_HIP_EINVAL, "null buffer");
+  if (tier != LLB_MOE_EXACT && tier != LLB_MOE_Q8) return fail(LLB_HIP_EINVAL, "unknown tier %d", tier);
+  if (scratch_bytes < llb_moe_hip_scratch_bytes(L, T, tier))
+    return fail(LLB_HIP_ESCRATCH, "scratch %zu < %zu bytes", scratch_bytes, llb_moe_hip_scratch_bytes(L, T, tier));
+  uint8_t* sc = dp<uint8_t>(scratch);
+  const ExactScratch s = exact_layout(L, T);
+  if ((rc = route(L, T, dp<float>(h2), dp<uint32_t>(ids), dp<float>(wt), sc, s))) return rc;
+  const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
+  const uint64_t rbg = row_bytes(fg, L->dm), rbu = row_bytes(fu, L->dm);
+  const uint64_t esg = (uint64_t)(fz ? 2 : 1) * L->ef * rbg;
+  const uint8_t* G = dp<uint8_t>(L->G);
+  const uint8_t* U = fz ? G + (uint64_t)L->ef * rbg : dp<uint8_t>(L->U);
+  if (tier == LLB_MOE_Q8) {
+    rc = moe_q8_forward(L, T, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt),
+                        (const float*)(sc + s.sgo), sc + s.total, g_stream);
+    return launched(rc, "q8 tier");
+  }
+  GuArgs g{};
+  g.G = G;
+  g.U = U;
+  // the expert stride: fused stacks hold gate and up rows per expert (llb_host.c:636)
+  g.rbg = rbg;
+  g.rbu = rbu;
+  g.dm = L->dm;
+  g.ef = L->ef;
+  g.nk = L->nk;
+  g.h2 = dp<float>(h2);
+  g.ids = dp<uint32_t>(ids);
+  g.act = (float*)(sc + s.act);
+  g.es = esg;
+  if ((rc = launched(launch_gu_exact(g, fg, fu, T * L->nk, g_stream), "expert gate/up"))) return rc;
+  DnArgs d{};
+  d.D = dp<uint8_t>(L->D);
+  d.rbd = row_bytes(fd, L->ef);
+  d.SD = dp<uint8_t>(L->SD);
+  d.rbs = L->sf ? row_bytes(L->fsd, L->sf) : 0;
+  d.dm = L->dm;
+  d.ef = L->ef;
+  d.nk = L->nk;
+  d.sf = L->sf;
+  d.rw = 64 / (L->nk + (L->sf ? 1 : 0));
+  d.act = g.act;
+  d.sa = (float*)(sc + s.sa);
+  d.ids = g.ids;
+  d.wt = dp<float>(wt);
+  d.sgo = (float*)(sc + s.sgo);
+  d.x1 = dp<float>(x1);
+  d.y = dp<float>(y);
+  return launched(launch_dn_exact(d, fd, L->sf ? L->fsd : 0, T, g_stream), "expert down + combine");
+}
+
+// ---------------------------------------------------------------- kernel-level entry points
+
+int llb_moe_hip_topk(llb_dptr lg, uint32_t lstride, uint32_t T, uint32_t ne, uint32_t nk, uint32_t has_sg,
+                     llb_dptr ids, llb_dptr wt, llb_dptr sgo) {
+  if (!ne || ne > 1024 || !nk || nk > ne || nk > 64 || lstride < ne + (has_sg ? 1 : 0))
+    return fail(LLB_HIP_EINVAL, "topk: need 1 <= nk <= min(ne, 64), ne <= 1024");
+  TopkArgs k{};
+  k.lg = dp<float>(lg);
+  k.lstride = lstride;
+  k.ne = ne;
+  k.nk = nk;
+  k.has_sg = has_sg;
+  k.ids = dp<uint32_t>(ids);
+  k.wt = dp<float>(wt);
+  k.sgo = dp<float>(sgo);
+  return launched(launch_topk(k, T, g_stream), "topk");
+}
+
+int llb_moe_hip_group(llb_dptr ids, uint32_t n, uint32_t nk, uint32_t ne, llb_dptr off, llb_dptr xmap, llb_dptr inv,
+                      llb_dptr scratch, size_t scratch_bytes) {
+  if (!ne || !nk || n % nk) return fail(LLB_HIP_EINVAL, "group: n must be a multiple of nk");
+  if (scratch_bytes < (size_t)(ne + 1) * 4) return fail(LLB_HIP_ESCRATCH, "group: scratch < (ne + 1) * 4 bytes");
+  return launched(launch_group(dp<uint32_t>(ids), n, nk, ne, dp<uint32_t>(off), dp<uint32_t>(xmap), dp<uint32_t>(inv),
+                               dp<uint32_t>(scratch), g_stream),
+                  "group");
+}
+
+int llb_moe_hip_q8_1(llb_dptr x, uint32_t n, llb_dptr q, llb_dptr ds) {
+  if (n % 32) return fail(LLB_HIP_EINVAL, "q8_1: n % 32 != 0");
+  return launched(launch_q8_1(dp<float>(x), n, dp<int8_t>(q), dp<float2>(ds), g_stream), "q8_1");
+}
+
+int llb_moe_hip_dequant(uint32_t fm, llb_dptr W, uint32_t rows, uint32_t cols, llb_dptr out) {
+  if (!row_bytes(fm, cols) || cols % 32 || (fm != LLB_FM_F32 && fm != LLB_FM_Q8_0 && cols % 256))
+    return fail(LLB_HIP_EINVAL, "dequant: bad format / width");
+  return launched(launch_dequant(fm, dp<uint8_t>(W), row_bytes(fm, cols), rows, cols, dp<float>(out), g_stream), "dequant");
+}
+
+int llb_moe_hip_gen_gauss(uint64_t seed, uint64_t stream, uint64_t i0, uint64_t n, float sigma, llb_dptr out) {
+  return launched(launch_gauss(seed, stream, i0, n, sigma, dp<float>(out), g_stream), "gen_gauss");
+}
+int llb_moe_hip_gen_rows(uint32_t fm, uint64_t seed, uint64_t stream, uint64_t r0, uint64_t nr, uint32_t cols,
+                         float sigma, llb_dptr out) {
+  if (!row_bytes(fm, cols)) return fail(LLB_HIP_EINVAL, "gen_rows: bad format");
+  return launched(launch_gen_rows(fm, seed, stream, r0, nr, cols, sigma, dp<uint8_t>(out), g_stream), "gen_rows");
+}
+
+}  // extern "C"

@@ -1,0 +1,76 @@
+// moe_kernels.h -- kernel argument blocks and launchers shared by the HIP sources and the C-ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+struct TreeSeg {
+  const uint8_t* W;  // rows of `cols` columns
+  uint64_t rb;       // row bytes
+  uint32_t rows;
+  float* out;        // out[t * ostride + row]
+  uint32_t ostride;
+};
+struct TreeArgs {
+  TreeSeg seg[4];
+  uint32_t cols;
+  const float* x;  // [T][xstride]
+  uint32_t T, xstride, tch;
+};
+struct TopkArgs {
+  const float* lg;  // [T][lstride]: ne logits, then the shared gate's when has_sg
+  uint32_t lstride, ne, nk, has_sg, sf;
+  uint32_t* ids;
+  float* wt;
+  float* sgo;
+  const float* gsu;  // [T][2 sf]: shared gate then up
+  float* sa;         // [T][sf]
+};
+struct GuArgs {
+  const uint8_t *G, *U;
+  uint64_t rbg, rbu;
+  uint64_t es;  // expert stride of G and U in bytes (fused stacks: 2 ef rows)
+  uint32_t dm, ef, nk;
+  const float* h2;  // [T][dm]
+  const uint32_t* ids;
+  float* act;  // [T nk][ef]
+};
+struct DnArgs {
+  const uint8_t* D;
+  uint64_t rbd;
+  const uint8_t* SD;
+  uint64_t rbs;
+  uint32_t dm, ef, nk, sf, rw;
+  const float* act;
+  const float* sa;
+  const uint32_t* ids;
+  const float* wt;
+  const float* sgo;
+  const float* x1;  // nullable
+  float* y;
+};
+
+int launch_tree_rows(const TreeArgs& a, uint32_t seg, uint32_t fm, uint32_t nsp, hipStream_t st);
+int launch_topk(const TopkArgs& a, uint32_t T, hipStream_t st);
+int launch_gu_exact(const GuArgs& a, uint32_t fg, uint32_t fu, uint32_t nslots, hipStream_t st);
+int launch_dn_exact(const DnArgs& a, uint32_t fd, uint32_t fs, uint32_t T, hipStream_t st);
+struct Q8Args {
+  const uint8_t *G, *U, *D, *SG, *SU, *SD;
+  uint64_t rbg, rbu, rbd, es, rbsg, rbsu, rbs;
+  uint32_t fg, fu, fd, fsg, fsu, fsd;
+  uint32_t dm, ef, nk, sf, rw;
+  const int8_t* hq;  // [T][dm] q8_1 of h2
+  const float2* hd;  // [T][dm / 32]
+  const uint32_t* ids;
+  const float* wt;
+  const float* sgo;
+  float* act;        // [T nk][ef]
+  int8_t* aq;        // [T nk][ef]
+  float2* ad;
+  float* sa;         // [T][sf]
+  int8_t* sq;
+  float2* sd2;
+  const float* x1;
+  float* y;
+};
+int launch_dequant(uint32_t fm, const uint8_t* W, uint64_t rb, uint32_t rows, uint32_t cols, float* out,
+                   hipStream_t st);

@@ -1,0 +1,299 @@
+// moe_q8.hip -- the q8 tier (the reference's LLB_MOE_DP4A decode tier and LLB_PREFILL=fast
+// numerics, host/llb_pf.cuh:447-620): expert products on q8_1 activations. A 32-column block's
+// dot is an int8 dot product (v_dot4_i32_i8) scaled in f32: Q4_K / Q5_K (d sc) xd acc - (dmin m) xs,
+// Q6_K d xd (sc0 a0 + sc1 a1), Q8_0 d xd acc. Routing stays the exact tier's. Tolerance class.
+// Also the dispatch permutation (llb_mx_group) and the q8_1 quantizer (pf_q8x).
+#include "../../include/llb_moe_hip.h"
+#include "moe_dev.h"
+#include "moe_kernels.h"
+
+// ---------------------------------------------------------------- q8_1 (pf_q8x)
+
+// one thread an element; lanes 32 h .. 32 h + 31 of a wave form one block: d = amax / 127,
+// q = round(x / d) (0 when amax = 0), s = sum x
+__global__ void __launch_bounds__(256) k_q8_1(const float* __restrict__ x, u32 n, signed char* __restrict__ q,
+                                              float2* __restrict__ ds) {
+  const u64 i = (u64)blockIdx.x * 256 + threadIdx.x;
+  const float v = i < n ? x[i] : 0.0f;
+  float a = fabsf(v), s = v;
+#pragma unroll
+  for (u32 m = 16; m > 0; m >>= 1) {
+    a = fmaxf(a, __shfl_xor(a, m, 64));
+    s = s + __shfl_xor(s, m, 64);
+  }
+  const float d = a / 127.0f;
+  if (i < n) q[i] = a == 0.0f ? (signed char)0 : (signed char)max(-127, min(127, (int)roundf(v / d)));
+  if (i < n && (threadIdx.x & 31) == 0) ds[i >> 5] = make_float2(d, s);
+}
+
+int launch_q8_1(const float* x, uint32_t n, int8_t* q, float2* ds, hipStream_t st) {
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_q8_1, dim3((n + 255) / 256), dim3(256), 0, st, x, n, (signed char*)q, ds);
+  return 0;
+}
+
+// ---------------------------------------------------------------- dispatch (llb_mx_group)
+
+// block e of ne: off[e] = #{slots with id < e}; then e's slots in ascending slot order, each
+// wave's ballot giving a slot its rank: xmap[pos] = slot / nk, inv[slot] = pos. Deterministic.
+__global__ void __launch_bounds__(256) k_group(const u32* __restrict__ ids, u32 n, u32 nk, u32 ne, u32* __restrict__ off,
+                                               u32* __restrict__ xmap, u32* __restrict__ inv) {
+  __shared__ u32 wc[4];
+  __shared__ u32 base;
+  const u32 e = blockIdx.x, t = threadIdx.x, w = t >> 6, L = t & 63;
+  u32 lt = 0;
+  for (u32 i = t; i < n; i += 256) lt += ids[i] < e ? 1u : 0u;
+#pragma unroll
+  for (u32 m = 32; m > 0; m >>= 1) lt += __shfl_xor(lt, m, 64);
+  if (L == 0) wc[w] = lt;
+  __syncthreads();
+  if (t == 0) {
+    base = wc[0] + wc[1] + wc[2] + wc[3];
+    off[e] = base;
+    if (e + 1 == ne) off[ne] = n;
+  }
+  __syncthreads();
+  for (u32 i0 = 0; i0 < n; i0 += 256) {
+    const u32 i = i0 + t;
+    const bool hit = i < n && ids[i] == e;
+    const u64 bal = __ballot(hit);
+    __syncthreads();
+    if (L == 0) wc[w] = (u32)__popcll(bal);
+    __syncthreads();
+    u32 before = base;
+    for (u32 k = 0; k < w; k++) before += wc[k];
+    const u32 at = before + (u32)__popcll(bal & ((1ull << L) - 1ull));
+    if (hit) {
+      xmap[at] = i / nk;
+      inv[i] = at;
+    }
+    __syncthreads();
+    if (t == 0) base += wc[0] + wc[1] + wc[2] + wc[3];
+    __syncthreads();
+  }
+}
+
+int launch_group(const uint32_t* ids, uint32_t n, uint32_t nk, uint32_t ne, uint32_t* off, uint32_t* xmap,
+                 uint32_t* inv, uint32_t* cnt, hipStream_t st) {
+  (void)cnt;
+  hipLaunchKernelGGL(k_group, dim3(ne), dim3(256), 0, st, ids, n, nk, ne, off, xmap, inv);
+  return 0;
+}
+
+// ---------------------------------------------------------------- block dots
+
+DEV int dot4(u32 a, u32 b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
+
+// 32-column block b of a row against 32 int8 x (8 dwords) with {d, s}
+template <u32 F> DEV float blk_q8(const u8* row, u32 b, const u32* xq, float2 e);
+
+template <> __device__ __forceinline__ float blk_q8<FM_Q4_K>(const u8* row, u32 b, const u32* xq, float2 e) {
+  const u8* B = row + (u64)(b >> 3) * 144u;
+  const u32 j = b & 7u;
+  const uint4 h = *(const uint4*)B;
+  const uint4* qp = (const uint4*)(B + 16 + 32 * (j >> 1));
+  const uint4 q0 = qp[0], q1 = qp[1];
+  const u32 q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+  const u32 sh = 4u * (j & 1u);
+  int acc = 0;
+#pragma unroll
+  for (int k = 0; k < 8; k++) acc = dot4((q[k] >> sh) & 0x0F0F0F0Fu, xq[k], acc);
+  u32 sc, mn;
+  k4_scmin(h, j, sc, mn);
+  return f16v(h.x & 0xffffu) * (float)sc * e.x * (float)acc - f16v(h.x >> 16) * (float)mn * e.y;
+}
+template <> __device__ __forceinline__ float blk_q8<FM_Q5_K>(const u8* row, u32 b, const u32* xq, float2 e) {
+  const u8* B = row + (u64)(b >> 3) * 176u;
+  const u32 j = b & 7u;
+  const uint4 h = *(const uint4*)B;
+  const uint4 h0 = *(const uint4*)(B + 16), h1 = *(const uint4*)(B + 32);
+  const uint4* qp = (const uint4*)(B + 48 + 32 * (j >> 1));
+  const uint4 q0 = qp[0], q1 = qp[1];
+  const u32 q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+  const u32 qh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+  const u32 sh = 4u * (j & 1u);
+  int acc = 0;
+#pragma unroll
+  for (int k = 0; k < 8; k++) acc = dot4(((q[k] >> sh) & 0x0F0F0F0Fu) | (((qh[k] >> j) & 0x01010101u) << 4), xq[k], acc);
+  u32 sc, mn;
+  k4_scmin(h, j, sc, mn);
+  return f16v(h.x & 0xffffu) * (float)sc * e.x * (float)acc - f16v(h.x >> 16) * (float)mn * e.y;
+}
+template <> __device__ __forceinline__ float blk_q8<FM_Q6_K>(const u8* row, u32 b, const u32* xq, float2 e) {
+  const u8* B = row + (u64)(b >> 3) * 210u;
+  const u32 bb = b & 7u, n = bb >> 2, quad = bb & 3u;
+  u32 ql[8], qh[8];
+  ld32_a2(B + 64 * n + 32 * (quad & 1u), ql);
+  ld32_a2(B + 128 + 32 * n, qh);
+  const u32 nsh = quad >= 2u ? 4u : 0u, hsh = 2u * quad;
+  int a0 = 0, a1 = 0;
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const u32 v = ((ql[k] >> nsh) & 0x0F0F0F0Fu) | (((qh[k] >> hsh) & 0x03030303u) << 4);
+    const u32 c = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;  // per byte q - 32, signed
+    if (k < 4) a0 = dot4(c, xq[k], a0);
+    else a1 = dot4(c, xq[k], a1);
+  }
+  const u32 scw = ld_u16(B + 192 + 8 * n + 2 * quad);
+  const float d = f16v(ld_u16(B + 208));
+  return d * e.x * ((float)(int)(signed char)(scw & 255u) * (float)a0 + (float)(int)(signed char)(scw >> 8) * (float)a1);
+}
+template <> __device__ __forceinline__ float blk_q8<FM_Q8_0>(const u8* row, u32 b, const u32* xq, float2 e) {
+  const u8* B = row + (u64)b * 34u;
+  const u32* a = (const u32*)((uintptr_t)B & ~(uintptr_t)3);
+  const bool odd = ((uintptr_t)B & 2u) != 0;
+  u32 v[9];
+#pragma unroll
+  for (int k = 0; k < 9; k++) v[k] = a[k];
+  int acc = 0;
+#pragma unroll
+  for (int k = 0; k < 8; k++) acc = dot4(odd ? v[k + 1] : __builtin_amdgcn_alignbit(v[k + 1], v[k], 16), xq[k], acc);
+  return f16v(odd ? v[0] >> 16 : v[0] & 0xffffu) * e.x * (float)acc;
+}
+
+// a row's q8 dot on the 4 lanes of a lane group: lane p takes blocks p, p + 4, ...
+template <u32 F>
+DEV float row_q8(const u8* row, u32 cols, const signed char* xq, const float2* xd, u32 p) {
+  float acc = 0.0f;
+  for (u32 b = p; b < cols / 32; b += 4) {
+    const uint4 a0 = *(const uint4*)(xq + 32 * b), a1 = *(const uint4*)(xq + 32 * b + 16);
+    const u32 x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    acc += blk_q8<F>(row, b, x, xd[b]);
+  }
+  acc += __shfl_xor(acc, 2, 64);
+  acc += __shfl_xor(acc, 1, 64);
+  return acc;
+}
+DEV float row_q8_fm(u32 f, const u8* row, u32 cols, const signed char* xq, const float2* xd, u32 p) {
+  switch (f) {
+    case FM_Q8_0: return row_q8<FM_Q8_0>(row, cols, xq, xd, p);
+    case FM_Q4_K: return row_q8<FM_Q4_K>(row, cols, xq, xd, p);
+    case FM_Q6_K: return row_q8<FM_Q6_K>(row, cols, xq, xd, p);
+    default: return row_q8<FM_Q5_K>(row, cols, xq, xd, p);
+  }
+}
+
+// ---------------------------------------------------------------- decode-shaped kernels (per slot)
+
+// gate + up + SwiGLU for each (token, rank) slot: 128 threads = 16 row pairs of one slot;
+// shared expert rows ride along as slot index T nk + t (its own weights, x of token t)
+__global__ void __launch_bounds__(128) k_gu_q8(Q8Args a, u32 nslot) {
+  const u32 task0 = blockIdx.x * 16;
+  const u32 L = threadIdx.x & 63, q = L >> 2, p = L & 3;
+  const u32 pr = 8 * (threadIdx.x >> 6) + (q & 7);
+  u32 slot, row, t, cols = a.dm;
+  const u8* w;
+  u32 f;
+  float* out;
+  if (task0 < nslot * a.ef) {
+    slot = task0 / a.ef;
+    row = task0 % a.ef + pr;
+    t = slot / a.nk;
+    const u64 e = a.ids[slot];
+    w = q < 8 ? a.G + e * a.es + row * a.rbg : a.U + e * a.es + row * a.rbu;
+    f = q < 8 ? a.fg : a.fu;
+    out = a.act + (u64)slot * a.ef + row;
+  } else {
+    const u32 k = task0 - nslot * a.ef;
+    t = k / a.sf;
+    row = k % a.sf + pr;
+    w = q < 8 ? a.SG + (u64)row * a.rbsg : a.SU + (u64)row * a.rbsu;
+    f = q < 8 ? a.fsg : a.fsu;
+    out = a.sa + (u64)t * a.sf + row;
+  }
+  const float v = row_q8_fm(f, w, cols, a.hq + (u64)t * a.dm, a.hd + (u64)t * (a.dm / 32), p);
+  const float u = __shfl_xor(v, 32, 64);
+  if (q < 8 && p == 0) *out = silu_mul(v, u);
+}
+
+// down + combine (llb_mx_dn + llb_mx_comb): rw rows of token blockIdx.y, tasks (j, r)
+__global__ void __launch_bounds__(256) k_dn_q8(Q8Args a) {
+  __shared__ float part[64];
+  const u32 t = blockIdx.y, nt = a.nk + (a.sf ? 1u : 0u);
+  const u32 g = threadIdx.x >> 2, p = threadIdx.x & 3;
+  if (g < a.rw * nt) {
+    const u32 j = g / a.rw, rl = g % a.rw, r = blockIdx.x * a.rw + rl;
+    if (r < a.dm) {
+      float v;
+      if (j < a.nk) {
+        const u64 slot = (u64)t * a.nk + j, e = a.ids[slot];
+        v = row_q8_fm(a.fd, a.D + (e * a.dm + r) * a.rbd, a.ef, a.aq + slot * a.ef, a.ad + slot * (a.ef / 32), p);
+      } else {
+        v = row_q8_fm(a.fsd, a.SD + (u64)r * a.rbs, a.sf, a.sq + (u64)t * a.sf, a.sd2 + (u64)t * (a.sf / 32), p);
+      }
+      if (p == 0) part[g] = v;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < a.rw) {
+    const u32 r = blockIdx.x * a.rw + threadIdx.x;
+    if (r < a.dm) {
+      const float* wt = a.wt + (u64)t * a.nk;
+      float mo = 0.0f;
+      for (u32 j = 0; j < a.nk; j++) {
+        const float v = part[j * a.rw + threadIdx.x];
+        mo = j == 0 ? v * wt[0] : mo + v * wt[j];
+      }
+      const float res = a.x1 ? a.x1[(u64)t * a.dm + r] : 0.0f;
+      a.y[(u64)t * a.dm + r] = a.sf ? (mo + part[a.nk * a.rw + threadIdx.x] * a.sgo[t]) + res : mo + res;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- the q8 layer
+
+static size_t al(size_t n) { return (n + 255) & ~(size_t)255; }
+static uint64_t rbytes(uint32_t fm, uint32_t cols) {
+  return fm == FM_Q8_0 ? (uint64_t)cols / 32 * 34 : fm == FM_Q4_K ? (uint64_t)cols / 256 * 144
+       : fm == FM_Q6_K ? (uint64_t)cols / 256 * 210 : fm == FM_Q5_K ? (uint64_t)cols / 256 * 176 : 0;
+}
+
+size_t moe_q8_scratch(const llb_moe_layer* L, uint32_t T) {
+  const size_t n = (size_t)T * L->nk;
+  return al((size_t)T * L->dm) + al((size_t)T * L->dm / 32 * 8) + al(n * L->ef * 4) + al(n * L->ef) +
+         al(n * L->ef / 32 * 8) + al((size_t)T * L->sf * 4 + 4) + al((size_t)T * L->sf + 4) + al((size_t)T * L->sf / 32 * 8 + 8);
+}
+
+int moe_q8_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const float* x1, float* y, const uint32_t* ids,
+                   const float* wt, const float* sgo, uint8_t* sc, hipStream_t st) {
+  const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
+  Q8Args a{};
+  const size_t n = (size_t)T * L->nk;
+  size_t o = 0;
+  a.hq = (const int8_t*)(sc + o); o += al((size_t)T * L->dm);
+  a.hd = (const float2*)(sc + o); o += al((size_t)T * L->dm / 32 * 8);
+  a.act = (float*)(sc + o); o += al(n * L->ef * 4);
+  a.aq = (int8_t*)(sc + o); o += al(n * L->ef);
+  a.ad = (float2*)(sc + o); o += al(n * L->ef / 32 * 8);
+  a.sa = (float*)(sc + o); o += al((size_t)T * L->sf * 4 + 4);
+  a.sq = (int8_t*)(sc + o); o += al((size_t)T * L->sf + 4);
+  a.sd2 = (float2*)(sc + o);
+  a.rbg = rbytes(fg, L->dm);
+  a.rbu = rbytes(fu, L->dm);
+  a.rbd = rbytes(fd, L->ef);
+  a.es = (uint64_t)(fz ? 2 : 1) * L->ef * a.rbg;
+  a.G = (const uint8_t*)(uintptr_t)L->G;
+  a.U = fz ? a.G + (uint64_t)L->ef * a.rbg : (const uint8_t*)(uintptr_t)L->U;
+  a.D = (const uint8_t*)(uintptr_t)L->D;
+  a.SG = (const uint8_t*)(uintptr_t)L->SG;
+  a.SU = (const uint8_t*)(uintptr_t)L->SU;
+  a.SD = (const uint8_t*)(uintptr_t)L->SD;
+  a.rbsg = L->sf ? rbytes(L->fsg, L->dm) : 0;
+  a.rbsu = L->sf ? rbytes(L->fsu, L->dm) : 0;
+  a.rbs = L->sf ? rbytes(L->fsd, L->sf) : 0;
+  a.fg = fg; a.fu = fu; a.fd = fd; a.fsg = L->fsg; a.fsu = L->fsu; a.fsd = L->fsd;
+  a.dm = L->dm; a.ef = L->ef; a.nk = L->nk; a.sf = L->sf;
+  a.rw = 64 / (L->nk + (L->sf ? 1 : 0));
+  a.ids = ids;
+  a.wt = wt;
+  a.x1 = x1;
+  a.y = y;
+  a.sgo = sgo;
+  launch_q8_1(h2, T * L->dm, (int8_t*)a.hq, (float2*)a.hd, st);
+  const uint32_t tasks = (uint32_t)(n * L->ef + (size_t)T * L->sf) / 16;
+  hipLaunchKernelGGL(k_gu_q8, dim3(tasks), dim3(128), 0, st, a, (u32)n);
+  launch_q8_1(a.act, (uint32_t)(n * L->ef), a.aq, a.ad, st);
+  if (L->sf) launch_q8_1(a.sa, T * L->sf, a.sq, a.sd2, st);
+  hipLaunchKernelGGL(k_dn_q8, dim3((L->dm + a.rw - 1) / a.rw, T), dim3(256), 0, st, a);
+  return 0;
+}

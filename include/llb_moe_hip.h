@@ -1,0 +1,109 @@
+/* llb_moe_hip.h -- C ABI of the MI355X (gfx950) MoE FFN backend.
+ *
+ * Drop-in boundary for eureka-engine's routed-expert FFN. The reference reaches this path through
+ * llb_moe_run (host/llb_host.c:622-724) and, for a prompt chunk, pf_moe (host/llb_pf.h:286-389),
+ * both over the backend contract of host/llb_backend.h:1-51 (realised for CUDA in
+ * host/llb_backend_cuda.h). This header gives
+ *   - that backend contract as plain functions (llb_hip_*),
+ *   - the layer entry points (llb_moe_hip_forward: decode, batched decode and prefill), and
+ *   - kernel-level entry points that replace the reference kernels one for one, for callers that
+ *     keep the reference's launch sequence.
+ * Plain pointers and sizes only. Device addresses are llb_dptr (u64), as in host/llb_backend.h:8-10.
+ * Every function returns 0 (or a non-zero dptr) on success and a negative code on failure;
+ * llb_hip_last_error() names the failure. Launches are queued in call order on the library's
+ * stream (llb_hip_set_stream; default the null stream), like the reference's null-stream launches.
+ */
+#ifndef LLB_MOE_HIP_H
+#define LLB_MOE_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint64_t llb_dptr; /* host/llb_backend.h:8-10 */
+
+/* error codes */
+#define LLB_HIP_OK 0
+#define LLB_HIP_EINVAL -1   /* a shape, format or argument outside the path's envelope */
+#define LLB_HIP_EDEVICE -2  /* a HIP runtime call failed */
+#define LLB_HIP_ESCRATCH -3 /* the scratch buffer is smaller than llb_moe_hip_scratch_bytes */
+
+/* format codes, host/llb_formats.h:4-14 */
+#define LLB_FM_F32 0
+#define LLB_FM_Q8_0 1
+#define LLB_FM_Q4_K 3
+#define LLB_FM_Q6_K 4
+#define LLB_FM_Q5_K 9
+
+/* numeric tiers */
+#define LLB_MOE_EXACT 0 /* the reference's exact tier: bit-identical to its f32 kernels */
+#define LLB_MOE_Q8 1    /* expert products on q8_1 activations (LLB_MOE_DP4A / LLB_PREFILL=fast) */
+
+/* ---- backend contract (host/llb_backend.h:8-41; CUDA twin host/llb_backend_cuda.h:186-219) ---- */
+int llb_hip_init(int device);                                  /* cuInit + context: gpu_load */
+const char* llb_hip_last_error(void);
+int llb_hip_set_stream(void* hip_stream);                      /* NULL: the null stream */
+llb_dptr llb_hip_alloc_zero(size_t bytes);                     /* llb_alloc_zero, llb_backend_cuda.h:186-191 */
+int llb_hip_free(llb_dptr p);                                  /* (the reference never frees) */
+int llb_hip_zero(llb_dptr p, size_t bytes);                    /* llb_zero */
+int llb_hip_copy(llb_dptr d, llb_dptr s, size_t bytes);        /* llb_copy */
+int llb_hip_write(llb_dptr d, const void* h, size_t bytes);    /* llb_write, llb_backend_cuda.h:210-213 */
+int llb_hip_read(void* h, llb_dptr p, size_t bytes);           /* llb_read, llb_backend_cuda.h:198-201 */
+int llb_hip_sync(void);                                        /* llb_sync, llb_backend_cuda.h:216-219 */
+int llb_hip_mem_info(size_t* free_bytes, size_t* total_bytes); /* cuMemGetInfo, host/llb_host.c:531 */
+
+/* ---- the layer ----
+ * What llb_moe_run reads from a layer's table row (host/llb_host.c:623-627, words of
+ * tools/gguf2pack.c:1142-1146) plus the device addresses llb_moe_load resolves
+ * (host/llb_host.c:491-586). Stacks are GGUF 3-D [ne][rows][row bytes] verbatim. */
+typedef struct {
+  uint32_t dm;  /* d_model (LlbShape.d) */
+  uint32_t ne;  /* word 27: expert count */
+  uint32_t nk;  /* word 30: experts used */
+  uint32_t ef;  /* word 28: expert ff */
+  uint32_t sf;  /* word 29: shared ff; 0 = no shared expert */
+  uint32_t fx;  /* word 26: gate | up << 4 | down << 8, bit 12 fused gate+up */
+  uint32_t fsg, fsu, fsd; /* shared gate / up / down formats (words 2..4 >> 28) */
+  uint32_t pad;
+  llb_dptr router; /* F32 [ne][dm] (word 21) */
+  llb_dptr shgate; /* F32 [dm] (word 22); 0 when sf == 0 */
+  llb_dptr G, U, D;    /* expert stacks; U ignored when fused (U = G + ef rows, llb_host.c:677) */
+  llb_dptr SG, SU, SD; /* shared expert */
+} llb_moe_layer;
+
+/* bytes of scratch llb_moe_hip_forward needs for T tokens at a tier (llb_scratch, host/llb_host.c:634) */
+size_t llb_moe_hip_scratch_bytes(const llb_moe_layer* L, uint32_t T, int tier);
+
+/* One MoE FFN layer over T tokens (llb_moe_run for T = 1, pf_moe's contract for a chunk).
+ * h2: [T][dm] f32 normalised FFN input; x1: [T][dm] residual (0: none); y: [T][dm] out,
+ * y = sum_j wt_j expert_j(h2) + sigmoid(sg) shared(h2) + x1.
+ * ids: [T][nk] u32 and wt: [T][nk] f32 out (the routing, as llb_moe_topk writes it).
+ * Routing is the exact tier's at every tier. Replaces host/llb_host.c:647-723 / host/llb_pf.h:286-389. */
+int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dptr x1, llb_dptr y, llb_dptr ids,
+                        llb_dptr wt, llb_dptr scratch, size_t scratch_bytes, int tier);
+
+/* ---- kernel-level entry points ---- */
+/* llb_moe_topk block 0 (tools/payload-moeany.patch:311-470) for T tokens: lg [T][lstride] (ne logits,
+ * then the shared gate's at index ne when has_sg) -> ids, wt [T][nk], sgo [T] */
+int llb_moe_hip_topk(llb_dptr lg, uint32_t lstride, uint32_t T, uint32_t ne, uint32_t nk, uint32_t has_sg,
+                     llb_dptr ids, llb_dptr wt, llb_dptr sgo);
+/* llb_mx_group (host/llb_pf.cuh:774-817): n = T nk slots -> off [ne+1], xmap [n], inv [n] */
+int llb_moe_hip_group(llb_dptr ids, uint32_t n, uint32_t nk, uint32_t ne, llb_dptr off, llb_dptr xmap, llb_dptr inv,
+                      llb_dptr scratch, size_t scratch_bytes);
+/* pf_q8x (tools/pf27/pfmm.cuh:39-54): n f32 (n % 32 == 0) -> q int8 [n], ds float2 {d, s} [n / 32] */
+int llb_moe_hip_q8_1(llb_dptr x, uint32_t n, llb_dptr q, llb_dptr ds);
+/* rows of a stack dequantized to f32 (the decoders the kernels use; q8g_w / q4k_w / q6k_w / q5k_w) */
+int llb_moe_hip_dequant(uint32_t fm, llb_dptr W, uint32_t rows, uint32_t cols, llb_dptr out);
+
+/* ---- synthetic data (benchmarks and tests): element i of stream s is a normal(0, sigma)
+ * from a hash of (seed, s, i); quantized rows use this project's quantizers ---- */
+int llb_moe_hip_gen_gauss(uint64_t seed, uint64_t stream, uint64_t i0, uint64_t n, float sigma, llb_dptr out);
+int llb_moe_hip_gen_rows(uint32_t fm, uint64_t seed, uint64_t stream, uint64_t r0, uint64_t nr, uint32_t cols,
+                         float sigma, llb_dptr out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,171 @@
+"""GPU parity of the HIP path against the CPU oracle, through the C ABI (include/llb_moe_hip.h).
+
+Exact tier: bit-exact ids, weights and layer outputs. q8 tier: tolerance (max rel 2e-3 class,
+cos >= 0.9999) against the oracle's q8 mode. Dequant and the generator: bit-exact bytes / values.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import eureka_moe as em
+import oracle_lib as ol
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+@pytest.mark.parametrize("fm,cols", [(em.F32, 2048), (em.Q8_0, 768), (em.Q8_0, 2048), (em.Q4_K, 2048),
+                                     (em.Q6_K, 512), (em.Q6_K, 768), (em.Q5_K, 1024)])
+def test_generator_and_dequant_bit_exact(dev, fm, cols):
+    _say("gen/dequant", fm, cols)
+    rows = 37
+    nb = rows * em.row_bytes(fm, cols)
+    p = dev.alloc(nb)
+    dev.check(dev.lib.llb_moe_hip_gen_rows(fm, 5, 3, 11, rows, cols, 0.02, p))
+    got = dev.read(p, nb, np.uint8)
+    want = ol.gen_rows(fm, 5, 3, 11, rows, cols)
+    assert np.array_equal(got, want)
+    out = dev.alloc(rows * cols * 4)
+    dev.check(dev.lib.llb_moe_hip_dequant(fm, p, rows, cols, out))
+    w = dev.read(out, (rows, cols), np.float32)
+    rb = em.row_bytes(fm, cols)
+    ref = np.stack([ol.deq(fm, want[r * rb:(r + 1) * rb], cols) for r in range(rows)])
+    assert np.array_equal(w.view(np.uint32), ref.view(np.uint32))
+    dev.free(p)
+    dev.free(out)
+
+
+def test_gauss_bit_exact(dev):
+    p = dev.alloc(10000 * 4)
+    dev.check(dev.lib.llb_moe_hip_gen_gauss(9, 4, 123, 10000, 1.0, p))
+    assert np.array_equal(dev.read(p, 10000, np.float32), ol.gauss(9, 4, 123, 10000))
+    dev.free(p)
+
+
+def _exact_case(dev, shape, seed, T, residual=True):
+    _say("exact", vars(shape), "seed", seed, "T", T)
+    layer = em.Layer(dev, shape, seed=seed)
+    run = em.Runner(dev, shape, T)
+    run.gen_inputs(seed)
+    run.forward(layer, residual=residual)
+    y, ids, wt = run.outputs()
+    run.free()
+    layer.free()
+    h2, x1 = ol.inputs(shape, seed, T)
+    hl = ol.HostLayer(shape, seed=seed, experts=[])
+    yr, idr, wtr, _ = hl.run(h2, x1 if residual else None)
+    return y, ids, wt, yr, idr, wtr, hl, h2
+
+
+SMALL = [
+    em.Shape(2048, 32, 4, 256, 256, em.Q4_K, em.Q4_K, em.Q6_K),
+    em.Shape(2048, 16, 2, 512, 0, em.Q8_0, em.Q8_0, em.Q8_0),
+    em.Shape(2048, 64, 6, 256, 512, em.Q5_K, em.Q5_K, em.Q5_K, fsg=em.Q5_K, fsu=em.Q5_K, fsd=em.Q4_K),
+    em.Shape(4096, 40, 8, 512, 256, em.Q6_K, em.Q6_K, em.Q8_0, fsg=em.Q6_K, fsu=em.Q6_K, fsd=em.Q6_K),
+    em.Shape(1280 + 256, 1000, 5, 256, 0, em.Q4_K, em.Q4_K, em.Q4_K),
+]
+
+
+@pytest.mark.parametrize("si", range(len(SMALL)))
+def test_exact_small_bit_exact(dev, si):
+    y, ids, wt, yr, idr, wtr, _, _ = _exact_case(dev, SMALL[si], seed=100 + si, T=3)
+    assert np.array_equal(ids, idr)
+    assert np.array_equal(wt.view(np.uint32), wtr.view(np.uint32))
+    assert np.array_equal(y.view(np.uint32), yr.view(np.uint32)), float(np.abs(y - yr).max())
+
+
+@pytest.mark.parametrize("name,seed", [("c1", 0), ("c2", 0), ("c2", 1), ("c1k", 3)])
+def test_exact_configs_bit_exact(dev, name, seed):
+    shape = em.SHAPES[name]
+    y, ids, wt, yr, idr, wtr, hl, h2 = _exact_case(dev, shape, seed, T=1, residual=False)
+    assert np.array_equal(ids, idr)
+    assert np.array_equal(wt.view(np.uint32), wtr.view(np.uint32))
+    assert np.array_equal(y.view(np.uint32), yr.view(np.uint32)), float(np.abs(y - yr).max())
+    m = ol.err_metrics(y, hl.f64(h2, ids))
+    _say(name, "vs float64", m)
+    assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999
+
+
+def test_exact_batched_bit_exact(dev):
+    y, ids, wt, yr, idr, wtr, _, _ = _exact_case(dev, em.SHAPES["c1"], seed=4, T=16)
+    assert np.array_equal(ids, idr)
+    assert np.array_equal(y.view(np.uint32), yr.view(np.uint32))
+
+
+def test_topk_kernel_ties_and_full(dev):
+    ne, nk = 96, 5
+    lg = np.zeros((3, ne + 1), np.float32)
+    lg[1, :ne] = np.arange(ne) % 7  # ties: the lower index wins
+    lg[2, :ne] = -np.arange(ne, dtype=np.float32)
+    p = dev.upload(lg)
+    ids, wt, sgo = dev.alloc(3 * nk * 4), dev.alloc(3 * nk * 4), dev.alloc(12)
+    dev.check(dev.lib.llb_moe_hip_topk(p, ne + 1, 3, ne, nk, 1, ids, wt, sgo))
+    gi = dev.read(ids, (3, nk), np.uint32)
+    gw = dev.read(wt, (3, nk), np.float32)
+    for t in range(3):
+        ri, rw, rs = np.zeros(nk, np.uint32), np.zeros(nk, np.float32), np.zeros(1, np.float32)
+        ol.lib().mo_topk(ol.ptr(lg[t].copy()), ne, nk, float(lg[t, ne]), ol.ptr(ri), ol.ptr(rw), ol.ptr(rs))
+        assert np.array_equal(gi[t], ri)
+        assert np.array_equal(gw[t].view(np.uint32), rw.view(np.uint32))
+    assert list(gi[0]) == list(range(nk))
+    assert list(gi[1]) == [6, 13, 20, 27, 34]
+
+
+@pytest.mark.parametrize("T,nk,ne", [(1, 8, 256), (64, 8, 128), (2048, 8, 128), (513, 10, 512)])
+def test_group_matches_stable_sort(dev, T, nk, ne):
+    rng = np.random.default_rng(T)
+    ids = np.stack([rng.permutation(ne)[:nk] for _ in range(T)]).astype(np.uint32).ravel()
+    n = ids.size
+    pi = dev.upload(ids)
+    off, xm, inv, sc = dev.alloc((ne + 1) * 4), dev.alloc(n * 4), dev.alloc(n * 4), dev.alloc((ne + 1) * 4)
+    dev.check(dev.lib.llb_moe_hip_group(pi, n, nk, ne, off, xm, inv, sc, (ne + 1) * 4))
+    go = dev.read(off, ne + 1, np.uint32)
+    gx = dev.read(xm, n, np.uint32)
+    gv = dev.read(inv, n, np.uint32)
+    ro, rx, rv = np.zeros(ne + 1, np.uint32), np.zeros(n, np.uint32), np.zeros(n, np.uint32)
+    ol.lib().mo_group(ol.ptr(ids), n, nk, ne, ol.ptr(ro), ol.ptr(rx), ol.ptr(rv))
+    assert np.array_equal(go, ro) and np.array_equal(gx, rx) and np.array_equal(gv, rv)
+    order = np.argsort(ids, kind="stable")
+    assert np.array_equal(rx, order // nk)
+
+
+def test_q8_1_matches_oracle(dev):
+    x = ol.gauss(3, 1, 0, 4096)
+    x[64:96] = 0.0
+    px = dev.upload(x)
+    q, ds = dev.alloc(4096), dev.alloc(4096 // 32 * 8)
+    dev.check(dev.lib.llb_moe_hip_q8_1(px, 4096, q, ds))
+    gq = dev.read(q, 4096, np.int8)
+    gds = dev.read(ds, (128, 2), np.float32)
+    rq, rd, rs = np.zeros(4096, np.int8), np.zeros(128, np.float32), np.zeros(128, np.float32)
+    ol.lib().mo_q8_1(ol.ptr(x), 4096, ol.ptr(rq), ol.ptr(rd), ol.ptr(rs))
+    assert np.array_equal(gq, rq)
+    assert np.array_equal(gds[:, 0], rd)
+    assert np.allclose(gds[:, 1], rs, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("name,T", [("c2", 1), ("c1", 4), ("c2", 8)])
+def test_q8_tier_tolerance(dev, name, T):
+    shape = em.SHAPES[name]
+    _say("q8", name, T)
+    layer = em.Layer(dev, shape, seed=2)
+    run = em.Runner(dev, shape, T, tier=em.Q8)
+    run.gen_inputs(2)
+    run.forward(layer, residual=False)
+    y, ids, wt = run.outputs()
+    run.free()
+    layer.free()
+    h2, _ = ol.inputs(shape, 2, T)
+    hl = ol.HostLayer(shape, seed=2, experts=[])
+    yq, idq, _, _ = hl.run(h2, None, tier="q8")
+    assert np.array_equal(ids, idq)
+    m = ol.err_metrics(y, yq)
+    _say("q8 vs oracle q8", m)
+    assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999
+    m64 = ol.err_metrics(y, hl.f64(h2, ids))
+    _say("q8 vs float64", m64)
+    assert m64["cos"] >= 0.999
