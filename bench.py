@@ -1,0 +1,167 @@
+"""Benchmark of the MoE FFN hot path on one MI355X (BASELINE.json metric: MoE layer us/token at
+decode + prefill tok/s, each against the HBM / MFMA roofline).
+
+Default workload: the Qwen3.5-35B-A3B-like layer -- hidden 2048, 256 experts,
+top-8, expert ff 512, shared expert 512, gate/up Q4_K, down Q6_K -- decoding one token through
+40 independently seeded layers resident in HBM (about 21 GB of expert stacks, far past the caches).
+A step = one token through the 40 layers; value = microseconds per token-layer.
+
+  python bench.py [--steps K] [--warmup W] [--layers L] [--config c2] [--tier exact|q8] [--no-cpu]
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "eureka-engine_amd"), os.path.join(ROOT, "tests")]
+
+import numpy as np  # noqa: E402
+
+import eureka_moe as em  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+
+
+def stage_bytes(shape, T=1):
+    """algorithmic HBM bytes per launch of each stage for T = 1 decode (every selected expert distinct)."""
+    s = shape
+    rbg, rbu, rbd = em.row_bytes(s.fg, s.dm), em.row_bytes(s.fu, s.dm), em.row_bytes(s.fd, s.ef)
+    route = s.ne * s.dm * 4
+    gate_up = s.nk * s.ef * (rbg + rbu)
+    down = s.nk * s.dm * rbd
+    if s.sf:
+        route += s.dm * 4 + s.sf * (em.row_bytes(s.fsg, s.dm) + em.row_bytes(s.fsu, s.dm))
+        down += s.dm * em.row_bytes(s.fsd, s.sf)
+    return {"route": route, "gate_up": gate_up, "down": down}
+
+
+def cpu_baseline(shape, seconds=12.0):
+    """the CPU oracle's exact layer, single thread, on tokens of layer 0 (experts generated first)."""
+    import oracle_lib as ol
+    hl = ol.HostLayer(shape, seed=0, layer=0, experts=[])
+    n, spent, t = 0, 0.0, 0
+    while spent < seconds and n < 64:
+        h2 = ol.gauss(0, ol.ST_H2, t * shape.dm, shape.dm).reshape(1, shape.dm)
+        ids, _, _ = hl.route(h2)
+        hl.add_experts(np.unique(ids))
+        hl._mk()
+        y = np.zeros((1, shape.dm), np.float32)
+        i2, w2, s2 = np.zeros((1, shape.nk), np.uint32), np.zeros((1, shape.nk), np.float32), np.zeros(1, np.float32)
+        t0 = time.perf_counter()
+        rc = ol.lib().mo_moe_exact(C.byref(hl.desc), 1, ol.ptr(h2), None, ol.ptr(y), ol.ptr(i2), ol.ptr(w2), ol.ptr(s2), 1)
+        spent += time.perf_counter() - t0
+        assert rc == 0
+        n += 1
+        t += 1
+    return {"value": spent / n * 1e6, "unit": "us/token-layer", "cores": 1, "kind": "port",
+            "sample": f"{n} decode tokens of one {shape.ne}-expert layer through the oracle's exact tier "
+                      f"(oracle/moe_oracle.c, -O2 -ffp-contract=off, 1 thread); expert generation outside the timer"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=40)
+    ap.add_argument("--config", default="c2")
+    ap.add_argument("--tier", default="exact", choices=["exact", "q8"])
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", dest="graph", action="store_false", help="launch per layer instead of a graph")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the MoE path is not sharded across GPUs); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    shape = em.SHAPES[args.config]
+    tier = em.EXACT if args.tier == "exact" else em.Q8
+    dev = em.Device(0)
+    layers = [em.Layer(dev, shape, seed=0, layer=i) for i in range(args.layers)]
+    T = 1
+    h2 = dev.alloc(args.layers * shape.dm * 4)
+    x1 = dev.alloc(args.layers * shape.dm * 4)
+    for i in range(args.layers):
+        dev.check(dev.lib.llb_moe_hip_gen_gauss(0, i * 16 + em.ST_H2, 0, shape.dm, 1.0, h2 + i * shape.dm * 4))
+        dev.check(dev.lib.llb_moe_hip_gen_gauss(0, i * 16 + em.ST_X1, 0, shape.dm, 1.0, x1 + i * shape.dm * 4))
+    y = dev.alloc(args.layers * shape.dm * 4)
+    ids = dev.alloc(args.layers * shape.nk * 4)
+    wt = dev.alloc(args.layers * shape.nk * 4)
+    sb = dev.lib.llb_moe_hip_scratch_bytes(C.byref(layers[0].desc), T, tier)
+    sc = dev.alloc(sb)
+    dev.sync()
+
+    def step():
+        for i, L in enumerate(layers):
+            dev.check(dev.lib.llb_moe_hip_forward(C.byref(L.desc), T, h2 + i * shape.dm * 4, x1 + i * shape.dm * 4,
+                                                  y + i * shape.dm * 4, ids + i * shape.nk * 4, wt + i * shape.nk * 4,
+                                                  sc, sb, tier))
+
+    run = step
+    if args.graph:
+        g = dev.capture(step)  # one token through every layer as one HIP graph (llb_graph_begin / end)
+        run = lambda: dev.replay(g)  # noqa: E731
+    for _ in range(args.warmup):
+        run()
+    dev.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run()
+    dev.sync()
+    wall = time.perf_counter() - t0
+    us_layer = wall / (args.steps * args.layers) * 1e6
+
+    # the same steps again with HIP events around each stage (recorded into the graph), for the
+    # per-kernel roofline: each stage interval is one kernel launch (route: its four tree launches)
+    nl = min(args.layers, 64)
+    sub = lambda: [dev.check(dev.lib.llb_moe_hip_forward(  # noqa: E731
+        C.byref(layers[i].desc), T, h2 + i * shape.dm * 4, x1 + i * shape.dm * 4, y + i * shape.dm * 4,
+        ids + i * shape.nk * 4, wt + i * shape.nk * 4, sc, sb, tier)) for i in range(nl)]
+    if args.graph:
+        dev.timing(2)
+        gt = dev.capture(sub)
+        for _ in range(args.steps):
+            dev.replay(gt)
+            dev.sync()
+            stages = dev.timing_read()
+    else:
+        dev.timing(1)
+        sub()
+        stages = dev.timing_read()
+    dev.timing(False)
+
+    sbytes = stage_bytes(shape)
+    dom = max(("gate_up", "down"), key=lambda k: stages.get(k, (0, 0))[0])
+    dom_us = stages[dom][0]
+    ach = sbytes[dom] / (dom_us * 1e-6) / 1e9
+    layer_bytes = sum(sbytes.values())
+    out = {
+        "metric": f"moe_layer_us_per_token_decode_{args.config}",
+        "value": round(us_layer, 3),
+        "unit": "us/token-layer",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32" if tier == em.EXACT else "int8",
+        "data": "synthetic: weights N(0,0.02) quantized on the device by this project's quantizers, x N(0,1)",
+        "config": {"workload": f"{args.config} decode, 1 token through {args.layers} resident layers, {args.tier} tier"
+                                f"{', one HIP graph a step' if args.graph else ', eager launches'}",
+                   "dm": shape.dm, "ne": shape.ne, "nk": shape.nk, "ef": shape.ef, "sf": shape.sf,
+                   "formats": {"gate": shape.fg, "up": shape.fu, "down": shape.fd}},
+        "layer_gbs": round(layer_bytes / (us_layer * 1e-6) / 1e9, 1),
+        "layer_frac_hbm": round(layer_bytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "stages_us": {k: round(v[0], 3) for k, v in stages.items()},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": sbytes[dom]},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(shape)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

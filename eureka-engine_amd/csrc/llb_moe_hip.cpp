@@ -22,6 +22,46 @@ int launch_q8_1(const float* x, uint32_t n, int8_t* q, float2* ds, hipStream_t s
 static thread_local char g_err[512];
 static hipStream_t g_stream = nullptr;
 
+// optional per-stage timing: an event pair around each stage of a forward, read after a sync
+static const char* g_stage_name[ST_NSTAGE] = {"route", "topk", "gate_up", "down", "q8_1"};
+static bool g_timing = false;
+static bool g_capturing = false;
+struct StageEv {
+  hipEvent_t a[64], b[64];
+  int n;
+  double us;
+  long cnt;
+};
+static StageEv g_ev[ST_NSTAGE];
+static bool g_keep = false;  // timing mode 2: the events live in a captured graph, keep them
+void stage_begin(int s) {
+  if (!g_timing) return;
+  StageEv& e = g_ev[s];
+  if (e.n >= 64) return;
+  if (!e.a[e.n]) { (void)hipEventCreate(&e.a[e.n]); (void)hipEventCreate(&e.b[e.n]); }
+  (void)hipEventRecord(e.a[e.n], g_stream);
+}
+void stage_end(int s) {
+  if (!g_timing) return;
+  StageEv& e = g_ev[s];
+  if (e.n >= 64) return;
+  (void)hipEventRecord(e.b[e.n], g_stream);
+  e.n++;
+}
+static void stage_collect() {
+  for (int s = 0; s < ST_NSTAGE; s++) {
+    StageEv& e = g_ev[s];
+    for (int i = 0; i < e.n; i++) {
+      float ms = 0;
+      if (hipEventSynchronize(e.b[i]) == hipSuccess && hipEventElapsedTime(&ms, e.a[i], e.b[i]) == hipSuccess) {
+        e.us += 1000.0 * ms;
+        e.cnt++;
+      }
+    }
+    if (!g_keep) e.n = 0;
+  }
+}
+
 static int fail(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -103,6 +143,43 @@ int llb_hip_read(void* h, llb_dptr p, size_t bytes) {
   return rc ? rc : hip_ok(hipStreamSynchronize(g_stream), "llb_read");
 }
 int llb_hip_sync(void) { return hip_ok(hipStreamSynchronize(g_stream), "llb_sync"); }
+
+// graph record / replay (llb_graph_begin / llb_graph_end, host/llb_backend_cuda.h:125-184): the
+// launches between begin and end are captured from the library's stream (a capture needs a
+// non-null stream: the library makes its own when none is set) and replayed as one graph
+static hipStream_t g_own = nullptr;
+int llb_hip_graph_begin(void) {
+  if (g_capturing) return fail(LLB_HIP_EINVAL, "graph_begin: already capturing");
+  if (!g_stream) {
+    if (!g_own) {
+      int rc = hip_ok(hipStreamCreateWithFlags(&g_own, hipStreamNonBlocking), "hipStreamCreate");
+      if (rc) return rc;
+    }
+    g_stream = g_own;
+  }
+  int rc = hip_ok(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  if (rc == 0) g_capturing = true;
+  return rc;
+}
+int llb_hip_graph_end(uint64_t* handle) {
+  if (!g_capturing) return fail(LLB_HIP_EINVAL, "graph_end: not capturing");
+  g_capturing = false;
+  hipGraph_t g = nullptr;
+  int rc = hip_ok(hipStreamEndCapture(g_stream, &g), "hipStreamEndCapture");
+  if (rc) return rc;
+  hipGraphExec_t x = nullptr;
+  rc = hip_ok(hipGraphInstantiate(&x, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+  (void)hipGraphDestroy(g);
+  if (rc) return rc;
+  *handle = (uint64_t)(uintptr_t)x;
+  return 0;
+}
+int llb_hip_graph_launch(uint64_t handle) {
+  return hip_ok(hipGraphLaunch((hipGraphExec_t)(uintptr_t)handle, g_stream), "hipGraphLaunch");
+}
+int llb_hip_graph_free(uint64_t handle) {
+  return hip_ok(hipGraphExecDestroy((hipGraphExec_t)(uintptr_t)handle), "hipGraphExecDestroy");
+}
 int llb_hip_mem_info(size_t* f, size_t* t) { return hip_ok(hipMemGetInfo(f, t), "hipMemGetInfo"); }
 
 // ---------------------------------------------------------------- layer checks and scratch
@@ -171,10 +248,12 @@ static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* 
   a.seg[2] = TreeSeg{dp<uint8_t>(L->SG), row_bytes(L->fsg, L->dm), L->sf, gsu, 2 * L->sf};
   a.seg[3] = TreeSeg{dp<uint8_t>(L->SU), row_bytes(L->fsu, L->dm), L->sf, gsu + L->sf, 2 * L->sf};
   int rc;
+  stage_begin(ST_ROUTE);
   if ((rc = launched(launch_tree_rows(a, 0, LLB_FM_F32, ns, g_stream), "router"))) return rc;
   if ((rc = launched(launch_tree_rows(a, 1, LLB_FM_F32, ns, g_stream), "shared gate logit"))) return rc;
   if ((rc = launched(launch_tree_rows(a, 2, L->fsg, ns, g_stream), "shared gate"))) return rc;
   if ((rc = launched(launch_tree_rows(a, 3, L->fsu, ns, g_stream), "shared up"))) return rc;
+  stage_end(ST_ROUTE);
   TopkArgs k{};
   k.lg = lg;
   k.lstride = L->ne + 1;
@@ -187,7 +266,10 @@ static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* 
   k.sgo = (float*)(sc + s.sgo);
   k.gsu = gsu;
   k.sa = (float*)(sc + s.sa);
-  return launched(launch_topk(k, T, g_stream), "topk");
+  stage_begin(ST_TOPK);
+  rc = launched(launch_topk(k, T, g_stream), "topk");
+  stage_end(ST_TOPK);
+  return rc;
 }
 
 int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dptr x1, llb_dptr y, llb_dptr ids,
@@ -225,7 +307,9 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
   g.ids = dp<uint32_t>(ids);
   g.act = (float*)(sc + s.act);
   g.es = esg;
+  stage_begin(ST_GU);
   if ((rc = launched(launch_gu_exact(g, fg, fu, T * L->nk, g_stream), "expert gate/up"))) return rc;
+  stage_end(ST_GU);
   DnArgs d{};
   d.D = dp<uint8_t>(L->D);
   d.rbd = row_bytes(fd, L->ef);
@@ -243,8 +327,29 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
   d.sgo = (float*)(sc + s.sgo);
   d.x1 = dp<float>(x1);
   d.y = dp<float>(y);
-  return launched(launch_dn_exact(d, fd, L->sf ? L->fsd : 0, T, g_stream), "expert down + combine");
+  stage_begin(ST_DN);
+  rc = launched(launch_dn_exact(d, fd, L->sf ? L->fsd : 0, T, g_stream), "expert down + combine");
+  stage_end(ST_DN);
+  return rc;
 }
+
+// per-stage timing (diagnostics and the benchmark's per-kernel roofline): on = 1 starts a fresh
+// tally; read returns the mean microseconds of each stage and the stage names
+int llb_moe_hip_timing(int on) {
+  g_timing = on != 0;
+  g_keep = on == 2;
+  for (int s = 0; s < ST_NSTAGE; s++) { g_ev[s].n = 0; g_ev[s].us = 0; g_ev[s].cnt = 0; }
+  return 0;
+}
+int llb_moe_hip_timing_read(double* mean_us, long* counts, int n) {
+  stage_collect();
+  for (int s = 0; s < ST_NSTAGE && s < n; s++) {
+    mean_us[s] = g_ev[s].cnt ? g_ev[s].us / g_ev[s].cnt : 0.0;
+    counts[s] = g_ev[s].cnt;
+  }
+  return ST_NSTAGE;
+}
+const char* llb_moe_hip_stage_name(int s) { return s >= 0 && s < ST_NSTAGE ? g_stage_name[s] : ""; }
 
 // ---------------------------------------------------------------- kernel-level entry points
 

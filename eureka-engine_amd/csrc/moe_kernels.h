@@ -3,6 +3,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+enum { ST_ROUTE, ST_TOPK, ST_GU, ST_DN, ST_Q8X, ST_NSTAGE };
+void stage_begin(int s);
+void stage_end(int s);
+
 struct TreeSeg {
   const uint8_t* W;  // rows of `cols` columns
   uint64_t rb;       // row bytes

@@ -53,6 +53,10 @@ _SIGS = {
     "llb_hip_read": (C.c_int, [C.c_void_p, C.c_uint64, C.c_size_t]),
     "llb_hip_sync": (C.c_int, []),
     "llb_hip_mem_info": (C.c_int, [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
+    "llb_hip_graph_begin": (C.c_int, []),
+    "llb_hip_graph_end": (C.c_int, [C.POINTER(C.c_uint64)]),
+    "llb_hip_graph_launch": (C.c_int, [C.c_uint64]),
+    "llb_hip_graph_free": (C.c_int, [C.c_uint64]),
     "llb_moe_hip_scratch_bytes": (C.c_size_t, [C.POINTER(MoeLayer), C.c_uint32, C.c_int]),
     "llb_moe_hip_forward": (C.c_int, [C.POINTER(MoeLayer), C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64,
                                       C.c_uint64, C.c_uint64, C.c_size_t, C.c_int]),
@@ -62,6 +66,9 @@ _SIGS = {
                                     C.c_uint64, C.c_size_t]),
     "llb_moe_hip_q8_1": (C.c_int, [C.c_uint64, C.c_uint32, C.c_uint64, C.c_uint64]),
     "llb_moe_hip_dequant": (C.c_int, [C.c_uint32, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint64]),
+    "llb_moe_hip_timing": (C.c_int, [C.c_int]),
+    "llb_moe_hip_timing_read": (C.c_int, [C.POINTER(C.c_double), C.POINTER(C.c_long), C.c_int]),
+    "llb_moe_hip_stage_name": (C.c_char_p, [C.c_int]),
     "llb_moe_hip_gen_gauss": (C.c_int, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, C.c_float, C.c_uint64]),
     "llb_moe_hip_gen_rows": (C.c_int, [C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32,
                                        C.c_float, C.c_uint64]),
@@ -128,6 +135,29 @@ class Device:
 
     def set_stream(self, handle):
         self.check(self.lib.llb_hip_set_stream(C.c_void_p(handle) if handle else None))
+
+    def timing(self, on):
+        self.check(self.lib.llb_moe_hip_timing(1 if on else 0))
+
+    def timing_read(self):
+        """{stage name: (mean us, count)} of the stages timed since timing(True)."""
+        us = (C.c_double * 16)()
+        n = (C.c_long * 16)()
+        k = self.lib.llb_moe_hip_timing_read(us, n, 16)
+        return {self.lib.llb_moe_hip_stage_name(i).decode(): (us[i], n[i]) for i in range(k) if n[i]}
+
+    def capture(self, fn):
+        """fn's launches recorded as a graph: returns a handle for replay()."""
+        self.check(self.lib.llb_hip_graph_begin())
+        try:
+            fn()
+        finally:
+            h = C.c_uint64()
+            self.check(self.lib.llb_hip_graph_end(C.byref(h)))
+        return h.value
+
+    def replay(self, handle):
+        self.check(self.lib.llb_hip_graph_launch(handle))
 
     def mem_info(self):
         f, t = C.c_size_t(), C.c_size_t()

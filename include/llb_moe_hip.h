@@ -53,6 +53,13 @@ int llb_hip_write(llb_dptr d, const void* h, size_t bytes);    /* llb_write, llb
 int llb_hip_read(void* h, llb_dptr p, size_t bytes);           /* llb_read, llb_backend_cuda.h:198-201 */
 int llb_hip_sync(void);                                        /* llb_sync, llb_backend_cuda.h:216-219 */
 int llb_hip_mem_info(size_t* free_bytes, size_t* total_bytes); /* cuMemGetInfo, host/llb_host.c:531 */
+/* graph record / replay: llb_graph_begin / llb_graph_end (host/llb_backend_cuda.h:125-184). Launches
+ * between begin and end are captured (not run); launch replays them on the library's stream.
+ * No allocation, copy or read may happen inside a capture (the reference bails to eager there). */
+int llb_hip_graph_begin(void);
+int llb_hip_graph_end(uint64_t* handle);
+int llb_hip_graph_launch(uint64_t handle);
+int llb_hip_graph_free(uint64_t handle);
 
 /* ---- the layer ----
  * What llb_moe_run reads from a layer's table row (host/llb_host.c:623-627, words of
@@ -96,6 +103,15 @@ int llb_moe_hip_group(llb_dptr ids, uint32_t n, uint32_t nk, uint32_t ne, llb_dp
 int llb_moe_hip_q8_1(llb_dptr x, uint32_t n, llb_dptr q, llb_dptr ds);
 /* rows of a stack dequantized to f32 (the decoders the kernels use; q8g_w / q4k_w / q6k_w / q5k_w) */
 int llb_moe_hip_dequant(uint32_t fm, llb_dptr W, uint32_t rows, uint32_t cols, llb_dptr out);
+
+/* ---- per-stage timing (no counterpart in the reference; its LLB_STEP_US times whole steps,
+ * host/llb_host.c:2873-2891): on = 1 resets and starts a tally of HIP-event intervals around each
+ * stage of llb_moe_hip_forward (at most 64 per stage between reads); read syncs and returns the mean
+ * microseconds and counts per stage. on = 2: the events are recorded into a graph being captured and
+ * kept, so each read after a replay adds that replay's intervals. Stage names: llb_moe_hip_stage_name. */
+int llb_moe_hip_timing(int on);
+int llb_moe_hip_timing_read(double* mean_us, long* counts, int n);
+const char* llb_moe_hip_stage_name(int stage);
 
 /* ---- synthetic data (benchmarks and tests): element i of stream s is a normal(0, sigma)
  * from a hash of (seed, s, i); quantized rows use this project's quantizers ---- */
