@@ -114,23 +114,16 @@ def main():
     wall = time.perf_counter() - t0
     us_layer = wall / (args.steps * args.layers) * 1e6
 
-    # the same steps again with HIP events around each stage (recorded into the graph), for the
-    # per-kernel roofline: each stage interval is one kernel launch (route: its four tree launches)
+    # one more pass over the layers with HIP events around each stage, queued behind a bounded stall
+    # so the kernels run back to back: each stage interval is one kernel (route: its four tree rows)
     nl = min(args.layers, 64)
     sub = lambda: [dev.check(dev.lib.llb_moe_hip_forward(  # noqa: E731
         C.byref(layers[i].desc), T, h2 + i * shape.dm * 4, x1 + i * shape.dm * 4, y + i * shape.dm * 4,
         ids + i * shape.nk * 4, wt + i * shape.nk * 4, sc, sb, tier)) for i in range(nl)]
-    if args.graph:
-        dev.timing(2)
-        gt = dev.capture(sub)
-        for _ in range(args.steps):
-            dev.replay(gt)
-            dev.sync()
-            stages = dev.timing_read()
-    else:
-        dev.timing(1)
-        sub()
-        stages = dev.timing_read()
+    dev.timing(1)
+    dev.check(dev.lib.llb_hip_spin(20000))  # the host queues every launch while the GPU is held
+    sub()
+    stages = dev.timing_read()
     dev.timing(False)
 
     sbytes = stage_bytes(shape)

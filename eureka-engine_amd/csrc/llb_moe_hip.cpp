@@ -18,49 +18,10 @@ size_t moe_q8_scratch(const llb_moe_layer* L, uint32_t T);
 int launch_group(const uint32_t* ids, uint32_t n, uint32_t nk, uint32_t ne, uint32_t* off, uint32_t* xmap,
                  uint32_t* inv, uint32_t* cnt, hipStream_t st);
 int launch_q8_1(const float* x, uint32_t n, int8_t* q, float2* ds, hipStream_t st);
+int launch_spin(uint32_t us, hipStream_t st);
 
 static thread_local char g_err[512];
 static hipStream_t g_stream = nullptr;
-
-// optional per-stage timing: an event pair around each stage of a forward, read after a sync
-static const char* g_stage_name[ST_NSTAGE] = {"route", "topk", "gate_up", "down", "q8_1"};
-static bool g_timing = false;
-static bool g_capturing = false;
-struct StageEv {
-  hipEvent_t a[64], b[64];
-  int n;
-  double us;
-  long cnt;
-};
-static StageEv g_ev[ST_NSTAGE];
-static bool g_keep = false;  // timing mode 2: the events live in a captured graph, keep them
-void stage_begin(int s) {
-  if (!g_timing) return;
-  StageEv& e = g_ev[s];
-  if (e.n >= 64) return;
-  if (!e.a[e.n]) { (void)hipEventCreate(&e.a[e.n]); (void)hipEventCreate(&e.b[e.n]); }
-  (void)hipEventRecord(e.a[e.n], g_stream);
-}
-void stage_end(int s) {
-  if (!g_timing) return;
-  StageEv& e = g_ev[s];
-  if (e.n >= 64) return;
-  (void)hipEventRecord(e.b[e.n], g_stream);
-  e.n++;
-}
-static void stage_collect() {
-  for (int s = 0; s < ST_NSTAGE; s++) {
-    StageEv& e = g_ev[s];
-    for (int i = 0; i < e.n; i++) {
-      float ms = 0;
-      if (hipEventSynchronize(e.b[i]) == hipSuccess && hipEventElapsedTime(&ms, e.a[i], e.b[i]) == hipSuccess) {
-        e.us += 1000.0 * ms;
-        e.cnt++;
-      }
-    }
-    if (!g_keep) e.n = 0;
-  }
-}
 
 static int fail(int code, const char* fmt, ...) {
   va_list ap;
@@ -77,6 +38,49 @@ static int hip_ok(hipError_t e, const char* what) {
 static int launched(int rc, const char* what) {
   if (rc != 0) return fail(LLB_HIP_EINVAL, "%s: no kernel for this format / shape", what);
   return hip_ok(hipGetLastError(), what);
+}
+
+// optional per-stage timing: an event pair around each stage of a forward, read after a sync
+static const char* g_stage_name[ST_NSTAGE] = {"route", "topk", "gate_up", "down", "q8_1"};
+static bool g_timing = false;
+static bool g_capturing = false;
+struct StageEv {
+  hipEvent_t a[64], b[64];
+  int n;
+  double us;
+  long cnt;
+};
+static StageEv g_ev[ST_NSTAGE];
+void stage_begin(int s) {
+  if (!g_timing || g_capturing) return;
+  StageEv& e = g_ev[s];
+  if (e.n >= 64) return;
+  if (!e.a[e.n]) { (void)hipEventCreate(&e.a[e.n]); (void)hipEventCreate(&e.b[e.n]); }
+  (void)hipEventRecord(e.a[e.n], g_stream);
+}
+void stage_end(int s) {
+  if (!g_timing || g_capturing) return;
+  StageEv& e = g_ev[s];
+  if (e.n >= 64) return;
+  (void)hipEventRecord(e.b[e.n], g_stream);
+  e.n++;
+}
+static void stage_collect() {
+  for (int s = 0; s < ST_NSTAGE; s++) {
+    StageEv& e = g_ev[s];
+    for (int i = 0; i < e.n; i++) {
+      float ms = 0;
+      hipError_t r = hipEventSynchronize(e.b[i]);
+      if (r == hipSuccess) r = hipEventElapsedTime(&ms, e.a[i], e.b[i]);
+      if (r == hipSuccess) {
+        e.us += 1000.0 * ms;
+        e.cnt++;
+      } else {
+        hip_ok(r, "stage timing");
+      }
+    }
+    e.n = 0;
+  }
 }
 
 template <class T> static T* dp(llb_dptr p) { return reinterpret_cast<T*>((uintptr_t)p); }
@@ -177,6 +181,13 @@ int llb_hip_graph_end(uint64_t* handle) {
 int llb_hip_graph_launch(uint64_t handle) {
   return hip_ok(hipGraphLaunch((hipGraphExec_t)(uintptr_t)handle, g_stream), "hipGraphLaunch");
 }
+// a kernel that keeps the stream busy for `us` microseconds of wall clock (s_memrealtime, 100 MHz),
+// so that launches queued behind it run back to back: the stage timings then measure kernels, not
+// the host's launch rate. Bounded: it exits at its deadline whatever happens.
+int llb_hip_spin(uint32_t us) {
+  if (us > 100000) return fail(LLB_HIP_EINVAL, "spin: at most 100 ms");
+  return launched(launch_spin(us, g_stream), "spin");
+}
 int llb_hip_graph_free(uint64_t handle) {
   return hip_ok(hipGraphExecDestroy((hipGraphExec_t)(uintptr_t)handle), "hipGraphExecDestroy");
 }
@@ -243,16 +254,14 @@ static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* 
   a.xstride = L->dm;
   a.tch = 16;
   const uint32_t ns = 1u << (cdepth(L->dm) - 9);
-  a.seg[0] = TreeSeg{dp<uint8_t>(L->router), (uint64_t)L->dm * 4, L->ne, lg, L->ne + 1};
-  a.seg[1] = TreeSeg{dp<uint8_t>(L->shgate), (uint64_t)L->dm * 4, L->sf ? 1u : 0u, lg + L->ne, L->ne + 1};
-  a.seg[2] = TreeSeg{dp<uint8_t>(L->SG), row_bytes(L->fsg, L->dm), L->sf, gsu, 2 * L->sf};
-  a.seg[3] = TreeSeg{dp<uint8_t>(L->SU), row_bytes(L->fsu, L->dm), L->sf, gsu + L->sf, 2 * L->sf};
+  a.seg[0] = TreeSeg{dp<uint8_t>(L->router), LLB_FM_F32, (uint64_t)L->dm * 4, L->ne, lg, L->ne + 1};
+  a.seg[1] = TreeSeg{dp<uint8_t>(L->shgate), LLB_FM_F32, (uint64_t)L->dm * 4, L->sf ? 1u : 0u, lg + L->ne, L->ne + 1};
+  a.seg[2] = TreeSeg{dp<uint8_t>(L->SG), L->fsg, row_bytes(L->fsg, L->dm), L->sf, gsu, 2 * L->sf};
+  a.seg[3] = TreeSeg{dp<uint8_t>(L->SU), L->fsu, row_bytes(L->fsu, L->dm), L->sf, gsu + L->sf, 2 * L->sf};
+  a.nseg = 4;
   int rc;
   stage_begin(ST_ROUTE);
-  if ((rc = launched(launch_tree_rows(a, 0, LLB_FM_F32, ns, g_stream), "router"))) return rc;
-  if ((rc = launched(launch_tree_rows(a, 1, LLB_FM_F32, ns, g_stream), "shared gate logit"))) return rc;
-  if ((rc = launched(launch_tree_rows(a, 2, L->fsg, ns, g_stream), "shared gate"))) return rc;
-  if ((rc = launched(launch_tree_rows(a, 3, L->fsu, ns, g_stream), "shared up"))) return rc;
+  if ((rc = launched(launch_tree_rows(a, ns, g_stream), "router + shared gate / up"))) return rc;
   stage_end(ST_ROUTE);
   TopkArgs k{};
   k.lg = lg;
@@ -264,8 +273,6 @@ static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* 
   k.ids = ids;
   k.wt = wt;
   k.sgo = (float*)(sc + s.sgo);
-  k.gsu = gsu;
-  k.sa = (float*)(sc + s.sa);
   stage_begin(ST_TOPK);
   rc = launched(launch_topk(k, T, g_stream), "topk");
   stage_end(ST_TOPK);
@@ -319,9 +326,9 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
   d.ef = L->ef;
   d.nk = L->nk;
   d.sf = L->sf;
-  d.rw = 64 / (L->nk + (L->sf ? 1 : 0));
+  d.rw = dn_rows(L->nk, L->ef, L->sf);
   d.act = g.act;
-  d.sa = (float*)(sc + s.sa);
+  d.gsu = (float*)(sc + s.gsu);
   d.ids = g.ids;
   d.wt = dp<float>(wt);
   d.sgo = (float*)(sc + s.sgo);
@@ -337,7 +344,6 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
 // tally; read returns the mean microseconds of each stage and the stage names
 int llb_moe_hip_timing(int on) {
   g_timing = on != 0;
-  g_keep = on == 2;
   for (int s = 0; s < ST_NSTAGE; s++) { g_ev[s].n = 0; g_ev[s].us = 0; g_ev[s].cnt = 0; }
   return 0;
 }

@@ -8,7 +8,7 @@
 // columns c0 .. c0 + 31 (c0 % 32 == 0) with exactly the values of the reference's dequant
 // (q8g_w / q4k_w / q6k_w / q5k_w, tools/payload-moeany.patch:85-91, tools/quant-doors.patch:34-80,
 // tools/payload-anyshape.patch:54-81): every product there is exact, so an FMA that folds the
-// final subtract (Q4_K / Q5_K) or a rebias (Q6_K, Q8_0) rounds once, at the same place.
+// final subtract (Q4_K / Q5_K) rounds once, at the same place, and with the same sign of zero.
 //
 // Everything here is compiled with -ffp-contract=off: a float op written is a float op executed.
 #pragma once
@@ -31,10 +31,12 @@ DEV float bits_f(u32 u) { return __uint_as_float(u); }
 
 // llb_f16 (tools/quant-fix.patch:11-21): (m [+ 1024]) * 2^(e' - 25), exact; exponent 31 keeps
 // the mantissa as an f32 inf / NaN payload
+// the value of every finite / infinite half is what v_cvt_f32_f16 gives; a NaN keeps its payload
+// unquieted as llb_f16 does (a select, no branch)
 DEV float f16v(u32 h) {
-  const u32 e = (h >> 10) & 31u, m = h & 1023u, s = (h >> 15) << 31;
-  const float mag = (float)(e ? m + 1024u : m) * bits_f(((e ? e : 1u) + 102u) << 23);
-  return bits_f(e == 31u ? (s | 0x7f800000u | m << 13) : (__float_as_uint(mag) | s));
+  const float hw = (float)__builtin_bit_cast(_Float16, (unsigned short)h);
+  const u32 nan = ((h >> 15) << 31) | 0x7f800000u | (h & 1023u) << 13;
+  return bits_f(((h & 0x7c00u) == 0x7c00u && (h & 1023u)) ? nan : __float_as_uint(hw));
 }
 
 // byte k of v as an exact float (v_cvt_f32_ubyte{0..3})
@@ -54,16 +56,17 @@ DEV void ld32_a2(const u8* p, u32 o[8]) {
   for (int k = 0; k < 8; k++) o[k] = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
 }
 
-// ggml get_scale_min_k4 (tools/q4k.py:20-23) from the 12 scale bytes held in h.y, h.z, h.w
+// ggml get_scale_min_k4 (tools/q4k.py:20-23) from the 12 scale bytes held in h.y (bytes 0..3),
+// h.z (4..7), h.w (8..11): shifts and masks, no indexed array (a runtime index into a register array
+// becomes a compare / select chain)
 DEV void k4_scmin(uint4 h, u32 j, u32& sc, u32& mn) {
-  const u32 b[12] = {h.y & 255u, (h.y >> 8) & 255u, (h.y >> 16) & 255u, h.y >> 24,
-                     h.z & 255u, (h.z >> 8) & 255u, (h.z >> 16) & 255u, h.z >> 24,
-                     h.w & 255u, (h.w >> 8) & 255u, (h.w >> 16) & 255u, h.w >> 24};
+  const u32 k = 8u * (j & 3u);
+  const u32 A = (h.y >> k) & 255u, B = (h.z >> k) & 255u, Cc = (h.w >> k) & 255u;
   if (j < 4) {
-    sc = b[j] & 63u; mn = b[j + 4] & 63u;
+    sc = A & 63u; mn = B & 63u;
   } else {
-    sc = (b[j + 4] & 15u) | ((b[j - 4] >> 6) << 4);
-    mn = (b[j + 4] >> 4) | ((b[j] >> 6) << 4);
+    sc = (Cc & 15u) | ((A >> 6) << 4);
+    mn = (Cc >> 4) | ((B >> 6) << 4);
   }
 }
 
@@ -81,8 +84,9 @@ template <> struct Span<FM_F32> {
   }
 };
 
-// Q8_0 GGUF block c0 / 32: [f16 d][32 x i8]; w = q * d (exact: 11-bit d times a 7-bit q)
-// as fma(d, q + 128, -128 d), q + 128 the unsigned byte of q ^ 0x80
+// Q8_0 GGUF block c0 / 32: [f16 d][32 x i8]; w = q * d (exact: 11-bit d times a 7-bit q), q as
+// (the unsigned byte of q ^ 0x80) - 128, exact. (An FMA with a -128 d addend would give +0 where
+// q * d is -0.)
 template <> struct Span<FM_Q8_0> {
   DEV void w(const u8* row, u32 c0, float* w) {
     const u8* B = row + (u64)(c0 >> 5) * 34u;
@@ -92,12 +96,11 @@ template <> struct Span<FM_Q8_0> {
 #pragma unroll
     for (int k = 0; k < 9; k++) v[k] = a[k];
     const float d = f16v(odd ? v[0] >> 16 : v[0] & 0xffffu);
-    const float nd = d * -128.0f;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
       const u32 q = (odd ? v[k + 1] : __builtin_amdgcn_alignbit(v[k + 1], v[k], 16)) ^ 0x80808080u;
 #pragma unroll
-      for (int t = 0; t < 4; t++) w[4 * k + t] = __builtin_fmaf(d, ubyte(q, t), nd);
+      for (int t = 0; t < 4; t++) w[4 * k + t] = (ubyte(q, t) - 128.0f) * d;
     }
   }
 };
@@ -153,7 +156,7 @@ template <> struct Span<FM_Q5_K> {
 // Q6_K (210 B: ql[128], qh[64] @128, int8 scales[16] @192, f16 d @208; 2-aligned). Column c:
 // n = c / 128, quad = (c % 128) / 32, l = c % 32: low nibble bits from ql[64 n + 32 (quad & 1) + l]
 // (upper nibble when quad >= 2), two high bits from qh[32 n + l] >> 2 quad, scale sc[c / 16].
-// w = (d sc) (q - 32): d sc and the product are exact, so fma(d sc, q, -32 d sc) is that value
+// w = (d sc) (q - 32): d sc, q - 32 and their product are exact
 template <> struct Span<FM_Q6_K> {
   DEV void w(const u8* row, u32 c0, float* w) {
     const u8* B = row + (u64)(c0 >> 8) * 210u;
@@ -164,17 +167,50 @@ template <> struct Span<FM_Q6_K> {
     const u32 scw = ld_u16(B + 192 + 8 * n + 2 * quad);
     const float d = f16v(ld_u16(B + 208));
     const float ds0 = d * (float)(int)(signed char)(scw & 255u), ds1 = d * (float)(int)(signed char)(scw >> 8);
-    const float n0 = ds0 * -32.0f, n1 = ds1 * -32.0f;
     const u32 nsh = quad >= 2u ? 4u : 0u, hsh = 2u * quad;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
       const u32 v = ((ql[k] >> nsh) & 0x0F0F0F0Fu) | (((qh[k] >> hsh) & 0x03030303u) << 4);
 #pragma unroll
       for (int t = 0; t < 4; t++)
-        w[4 * k + t] = k < 4 ? __builtin_fmaf(ds0, ubyte(v, t), n0) : __builtin_fmaf(ds1, ubyte(v, t), n1);
+        w[4 * k + t] = (k < 4 ? ds0 : ds1) * (ubyte(v, t) - 32.0f);
     }
   }
 };
+
+// ---- cross-lane pair sums at ALU latency (DPP and the gfx950 permlane swaps; ds_bpermute, which
+// __shfl_xor uses, costs about 60 ns a step). xaddM(v) = v + v[lane ^ M]; IEEE addition commutes, so
+// the value is the exact pair sum. Lanes where it holds: M = 1, 2, 8, 16, 32 every lane; M = 4 the
+// lanes whose index mod 16 is < 4 or is 8..11 (row_ror:12 reads lane + 4 of the row).
+template <int CTRL> DEV float dppf(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL> DEV u32 dppu(u32 v) { return (u32)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false); }
+#define DPP_XOR1 0xB1   // quad_perm [1, 0, 3, 2]
+#define DPP_XOR2 0x4E   // quad_perm [2, 3, 0, 1]
+#define DPP_UP4 0x12C   // row_ror:12: lane l reads lane (l + 4) mod 16 of its row
+#define DPP_XOR8 0x128  // row_ror:8
+DEV float xadd1(float v) { return v + dppf<DPP_XOR1>(v); }
+DEV float xadd2(float v) { return v + dppf<DPP_XOR2>(v); }
+DEV float xadd4(float v) { return v + dppf<DPP_UP4>(v); }
+DEV float xadd8(float v) { return v + dppf<DPP_XOR8>(v); }
+DEV float xadd16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+DEV float xadd32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// lane ^ 32's value
+DEV float xpeer32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+}
+// moe_dot's tree over the 32 lanes of each half-wave, levels 16, 8, 4, 2, 1: exact at lanes 0, 32
+DEV float tree32_desc(float v) { return xadd1(xadd2(xadd4(xadd8(xadd16(v))))); }
+// the engine tree across a wave, levels 1, 2, 4, 8, 16, 32 (lower lane bits first): exact at lane 0
+DEV float tree64_asc(float v) { return xadd32(xadd16(xadd8(xadd4(xadd2(xadd1(v)))))); }
 
 // the leaf of every exact GEMV: (w0 x0 + w1 x1) + (w2 x2 + w3 x3)
 DEV float leaf4(const float* w, float4 x) {

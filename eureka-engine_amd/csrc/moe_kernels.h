@@ -9,6 +9,7 @@ void stage_end(int s);
 
 struct TreeSeg {
   const uint8_t* W;  // rows of `cols` columns
+  uint32_t fm;
   uint64_t rb;       // row bytes
   uint32_t rows;
   float* out;        // out[t * ostride + row]
@@ -16,6 +17,7 @@ struct TreeSeg {
 };
 struct TreeArgs {
   TreeSeg seg[4];
+  uint32_t nseg;
   uint32_t cols;
   const float* x;  // [T][xstride]
   uint32_t T, xstride, tch;
@@ -26,8 +28,6 @@ struct TopkArgs {
   uint32_t* ids;
   float* wt;
   float* sgo;
-  const float* gsu;  // [T][2 sf]: shared gate then up
-  float* sa;         // [T][sf]
 };
 struct GuArgs {
   const uint8_t *G, *U;
@@ -45,7 +45,7 @@ struct DnArgs {
   uint64_t rbs;
   uint32_t dm, ef, nk, sf, rw;
   const float* act;
-  const float* sa;
+  const float* gsu;  // [T][2 sf]: the shared gate then up dots (sa = silu(g) u is formed in the kernel)
   const uint32_t* ids;
   const float* wt;
   const float* sgo;
@@ -53,7 +53,8 @@ struct DnArgs {
   float* y;
 };
 
-int launch_tree_rows(const TreeArgs& a, uint32_t seg, uint32_t fm, uint32_t nsp, hipStream_t st);
+int launch_tree_rows(const TreeArgs& a, uint32_t nsp, hipStream_t st);
+uint32_t dn_rows(uint32_t nk, uint32_t ef, uint32_t sf);
 int launch_topk(const TopkArgs& a, uint32_t T, hipStream_t st);
 int launch_gu_exact(const GuArgs& a, uint32_t fg, uint32_t fu, uint32_t nslots, hipStream_t st);
 int launch_dn_exact(const DnArgs& a, uint32_t fd, uint32_t fs, uint32_t T, hipStream_t st);

@@ -303,3 +303,14 @@ int moe_q8_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const fl
   stage_end(ST_DN);
   return 0;
 }
+
+// ---------------------------------------------------------------- a bounded stall (timing aid)
+
+__global__ void k_spin(u64 ticks) {
+  const u64 t0 = __builtin_amdgcn_s_memrealtime();
+  while (__builtin_amdgcn_s_memrealtime() - t0 < ticks) __builtin_amdgcn_s_sleep(8);
+}
+int launch_spin(uint32_t us, hipStream_t st) {
+  hipLaunchKernelGGL(k_spin, dim3(1), dim3(64), 0, st, (u64)us * 100u);
+  return 0;
+}

@@ -67,6 +67,7 @@ _SIGS = {
     "llb_moe_hip_q8_1": (C.c_int, [C.c_uint64, C.c_uint32, C.c_uint64, C.c_uint64]),
     "llb_moe_hip_dequant": (C.c_int, [C.c_uint32, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint64]),
     "llb_moe_hip_timing": (C.c_int, [C.c_int]),
+    "llb_hip_spin": (C.c_int, [C.c_uint32]),
     "llb_moe_hip_timing_read": (C.c_int, [C.POINTER(C.c_double), C.POINTER(C.c_long), C.c_int]),
     "llb_moe_hip_stage_name": (C.c_char_p, [C.c_int]),
     "llb_moe_hip_gen_gauss": (C.c_int, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, C.c_float, C.c_uint64]),

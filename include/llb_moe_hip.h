@@ -107,8 +107,10 @@ int llb_moe_hip_dequant(uint32_t fm, llb_dptr W, uint32_t rows, uint32_t cols, l
 /* ---- per-stage timing (no counterpart in the reference; its LLB_STEP_US times whole steps,
  * host/llb_host.c:2873-2891): on = 1 resets and starts a tally of HIP-event intervals around each
  * stage of llb_moe_hip_forward (at most 64 per stage between reads); read syncs and returns the mean
- * microseconds and counts per stage. on = 2: the events are recorded into a graph being captured and
- * kept, so each read after a replay adds that replay's intervals. Stage names: llb_moe_hip_stage_name. */
+ * microseconds and counts per stage (eager launches only: nothing is timed inside a graph capture).
+ * llb_hip_spin(us) queues a kernel that holds the stream for us microseconds (bounded), so the launches
+ * behind it run back to back and the intervals measure the kernels. Stage names: llb_moe_hip_stage_name. */
+int llb_hip_spin(uint32_t us);
 int llb_moe_hip_timing(int on);
 int llb_moe_hip_timing_read(double* mean_us, long* counts, int n);
 const char* llb_moe_hip_stage_name(int stage);

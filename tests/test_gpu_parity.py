@@ -169,3 +169,55 @@ def test_q8_tier_tolerance(dev, name, T):
     m64 = ol.err_metrics(y, hl.f64(h2, ids))
     _say("q8 vs float64", m64)
     assert m64["cos"] >= 0.999
+
+
+def _nan_equal(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    ok = (np.isnan(a) & np.isnan(b)) | (a.view(np.uint32) == b.view(np.uint32))
+    if not ok.all():
+        bad = np.argwhere(~ok)[:5]
+        _say("mismatch at", bad.tolist(), [(float(a[tuple(i)]), float(b[tuple(i)])) for i in bad])
+    return bool(ok.all())
+
+
+def test_dequant_every_f16_scale(dev):
+    """every f16 bit pattern as a Q4_K super-block scale (d), and every finite one as a Q8_0 block
+    scale: the device decoders give the oracle's values (NaN against NaN)."""
+    rng = np.random.default_rng(0)
+    n = 65536
+    blk = np.zeros((n, 144), np.uint8)
+    blk[:, 0:2] = np.arange(n, dtype=np.uint16).view(np.uint8).reshape(n, 2)
+    blk[:, 2:4] = np.frombuffer(np.float16(0.25).tobytes(), np.uint8)
+    blk[:, 4:16] = rng.integers(0, 256, (n, 12), dtype=np.uint8)
+    blk[:, 16:] = rng.integers(0, 256, (n, 128), dtype=np.uint8)
+    p = dev.upload(blk)
+    out = dev.alloc(n * 256 * 4)
+    dev.check(dev.lib.llb_moe_hip_dequant(em.Q4_K, p, n, 256, out))
+    got = dev.read(out, (n, 256), np.float32)
+    ref = np.stack([ol.deq(em.Q4_K, blk[i], 256) for i in range(n)])
+    assert _nan_equal(got, ref)
+    dev.free(p)
+    dev.free(out)
+    h = np.arange(n, dtype=np.uint16)
+    m = h.size
+    q8 = np.zeros((m, 34), np.uint8)
+    q8[:, 0:2] = h.view(np.uint8).reshape(m, 2)
+    q8[:, 2:] = rng.integers(0, 256, (m, 32), dtype=np.uint8)
+    p = dev.upload(q8)
+    out = dev.alloc(m * 32 * 4)
+    dev.check(dev.lib.llb_moe_hip_dequant(em.Q8_0, p, m, 32, out))
+    got = dev.read(out, (m, 32), np.float32)
+    ref = np.stack([ol.deq(em.Q8_0, q8[i], 32) for i in range(m)])
+    assert _nan_equal(got, ref)
+    dev.free(p)
+    dev.free(out)
+    q6 = rng.integers(0, 256, (n, 210), dtype=np.uint8)
+    q6[:, 208:210] = np.arange(n, dtype=np.uint16).view(np.uint8).reshape(n, 2)
+    p = dev.upload(q6)
+    out = dev.alloc(n * 256 * 4)
+    dev.check(dev.lib.llb_moe_hip_dequant(em.Q6_K, p, n, 256, out))
+    got = dev.read(out, (n, 256), np.float32)
+    ref = np.stack([ol.deq(em.Q6_K, q6[i], 256) for i in range(n)])
+    assert _nan_equal(got, ref)
+    dev.free(p)
+    dev.free(out)
