@@ -221,7 +221,7 @@ static int check_layer(const llb_moe_layer* L, int tier) {
 static size_t al(size_t n) { return (n + 255) & ~(size_t)255; }
 
 struct ExactScratch {
-  size_t lg, gsu, sa, sgo, act, total;
+  size_t lg, gsu, sa, sgo, act, ctr, total;
 };
 static ExactScratch exact_layout(const llb_moe_layer* L, uint32_t T) {
   ExactScratch s;
@@ -231,6 +231,7 @@ static ExactScratch exact_layout(const llb_moe_layer* L, uint32_t T) {
   s.sa = o; o += al((size_t)T * L->sf * 4 + 4);
   s.sgo = o; o += al((size_t)T * 4);
   s.act = o; o += al((size_t)T * L->nk * L->ef * 4);
+  s.ctr = o; o += al(8 * 4);
   s.total = o;
   return s;
 }
@@ -279,6 +280,31 @@ static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* 
   return rc;
 }
 
+static int fused_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const float* x1, float* y, uint32_t* ids,
+                         float* wt, uint8_t* sc, const ExactScratch& s);
+
+// the fused one-launch layer (exact tier, small T) on by default; 0 forces the four-launch path
+static int g_fused = 0;
+static int g_ncu = 0;
+int llb_moe_hip_set_fused(int on) {
+  g_fused = on;
+  return 0;
+}
+int llb_moe_hip_status(llb_dptr scratch, const llb_moe_layer* L, uint32_t T) {
+  if (!scratch || !L || !T) return fail(LLB_HIP_EINVAL, "status: null argument");
+  const ExactScratch s = exact_layout(L, T);
+  uint32_t e = 0;
+  int rc = hip_ok(hipMemcpyAsync(&e, dp<uint8_t>(scratch) + s.ctr + 5 * 4, 4, hipMemcpyDeviceToHost, g_stream), "status");
+  if (!rc) rc = hip_ok(hipStreamSynchronize(g_stream), "status");
+  if (rc) return rc;
+  if (e) {
+    uint32_t z = 0;
+    (void)hipMemcpy(dp<uint8_t>(scratch) + s.ctr + 5 * 4, &z, 4, hipMemcpyHostToDevice);
+    return fail(LLB_HIP_EDEVICE, "fused layer: a phase wait timed out (results of that launch are not valid)");
+  }
+  return 0;
+}
+
 int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dptr x1, llb_dptr y, llb_dptr ids,
                         llb_dptr wt, llb_dptr scratch, size_t scratch_bytes, int tier) {
   int rc = check_layer(L, tier);
@@ -290,8 +316,11 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
     return fail(LLB_HIP_ESCRATCH, "scratch %zu < %zu bytes", scratch_bytes, llb_moe_hip_scratch_bytes(L, T, tier));
   uint8_t* sc = dp<uint8_t>(scratch);
   const ExactScratch s = exact_layout(L, T);
-  if ((rc = route(L, T, dp<float>(h2), dp<uint32_t>(ids), dp<float>(wt), sc, s))) return rc;
   const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
+  const uint32_t nsp = 1u << (cdepth(L->dm) - 9), fs = L->sf ? L->fsd : 0;
+  if (tier == LLB_MOE_EXACT && g_fused && T <= 8 && fg == fu && fused_supported(fg, fd, fs, nsp))
+    return fused_forward(L, T, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt), sc, s);
+  if ((rc = route(L, T, dp<float>(h2), dp<uint32_t>(ids), dp<float>(wt), sc, s))) return rc;
   const uint64_t rbg = row_bytes(fg, L->dm), rbu = row_bytes(fu, L->dm);
   const uint64_t esg = (uint64_t)(fz ? 2 : 1) * L->ef * rbg;
   const uint8_t* G = dp<uint8_t>(L->G);
@@ -337,6 +366,76 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
   stage_begin(ST_DN);
   rc = launched(launch_dn_exact(d, fd, L->sf ? L->fsd : 0, T, g_stream), "expert down + combine");
   stage_end(ST_DN);
+  return rc;
+}
+
+// the fused layer: the same four stages' argument blocks, one persistent launch
+static int fused_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const float* x1, float* y, uint32_t* ids,
+                         float* wt, uint8_t* sc, const ExactScratch& s) {
+  const uint32_t fg = L->fx & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
+  const uint64_t rbg = row_bytes(fg, L->dm);
+  FusedArgs f{};
+  float* lg = (float*)(sc + s.lg);
+  float* gsu = (float*)(sc + s.gsu);
+  f.tr.cols = L->dm;
+  f.tr.x = h2;
+  f.tr.T = T;
+  f.tr.xstride = L->dm;
+  f.tr.tch = 1;
+  f.tr.seg[0] = TreeSeg{dp<uint8_t>(L->router), LLB_FM_F32, (uint64_t)L->dm * 4, L->ne, lg, L->ne + 1};
+  f.tr.seg[1] = TreeSeg{dp<uint8_t>(L->shgate), LLB_FM_F32, (uint64_t)L->dm * 4, L->sf ? 1u : 0u, lg + L->ne, L->ne + 1};
+  f.tr.seg[2] = TreeSeg{dp<uint8_t>(L->SG), L->fsg, row_bytes(L->fsg, L->dm), L->sf, gsu, 2 * L->sf};
+  f.tr.seg[3] = TreeSeg{dp<uint8_t>(L->SU), L->fsu, row_bytes(L->fsu, L->dm), L->sf, gsu + L->sf, 2 * L->sf};
+  f.tr.nseg = 4;
+  const uint32_t rows = L->ne + (L->sf ? 1 + 2 * L->sf : 0);
+  f.tk = TopkArgs{lg, L->ne + 1, L->ne, L->nk, L->sf ? 1u : 0u, L->sf, ids, wt, (float*)(sc + s.sgo)};
+  f.gu.G = dp<uint8_t>(L->G);
+  f.gu.U = fz ? f.gu.G + (uint64_t)L->ef * rbg : dp<uint8_t>(L->U);
+  f.gu.rbg = rbg;
+  f.gu.rbu = row_bytes(L->fx >> 4 & 15, L->dm);
+  f.gu.es = (uint64_t)(fz ? 2 : 1) * L->ef * rbg;
+  f.gu.dm = L->dm;
+  f.gu.ef = L->ef;
+  f.gu.nk = L->nk;
+  f.gu.h2 = h2;
+  f.gu.ids = ids;
+  f.gu.act = (float*)(sc + s.act);
+  f.dn.D = dp<uint8_t>(L->D);
+  f.dn.rbd = row_bytes(fd, L->ef);
+  f.dn.SD = dp<uint8_t>(L->SD);
+  f.dn.rbs = L->sf ? row_bytes(L->fsd, L->sf) : 0;
+  f.dn.dm = L->dm;
+  f.dn.ef = L->ef;
+  f.dn.nk = L->nk;
+  f.dn.sf = L->sf;
+  f.dn.rw = dn_rows(L->nk, L->ef, L->sf);
+  f.dn.act = f.gu.act;
+  f.dn.gsu = gsu;
+  f.dn.ids = ids;
+  f.dn.wt = wt;
+  f.dn.sgo = (float*)(sc + s.sgo);
+  f.dn.x1 = x1;
+  f.dn.y = y;
+  f.T = T;
+  f.rpt = (rows + 7) / 8;
+  f.nR = T * f.rpt;
+  f.np = 4;
+  f.nG = T * L->nk * L->ef / f.np;
+  f.dpt = (L->dm + f.dn.rw - 1) / f.dn.rw;
+  f.nD = T * f.dpt;
+  f.spin = 20000000u;  // 0.2 s
+  f.ctr = (uint32_t*)(sc + s.ctr);
+  if (!g_ncu) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      n = 256;
+    g_ncu = n;
+  }
+  const uint32_t items = f.nR + T + f.nG + f.nD;
+  const uint32_t grid = items < (uint32_t)g_ncu * 4 ? items : (uint32_t)g_ncu * 4;
+  stage_begin(ST_GU);
+  int rc = launched(launch_fused(f, fg, fd, L->sf ? L->fsd : 0, 1u << (cdepth(L->dm) - 9), grid, g_stream), "fused layer");
+  stage_end(ST_GU);
   return rc;
 }
 

@@ -21,14 +21,13 @@
 // ---------------------------------------------------------------- tree rows (router, shared)
 
 template <u32 NSP>
-DEV float tree_row_lane(const float* w, const float* __restrict__ x, u32 c0base) {
+DEV float tree_row_lane(const float* w, const float4* xv) {
   float s[NSP];
 #pragma unroll
   for (u32 q = 0; q < NSP; q++) {
-    const float* xv = x + c0base + 32 * q;
     float l[8];
 #pragma unroll
-    for (u32 g = 0; g < 8; g++) l[g] = leaf4(w + 32 * q + 4 * g, *(const float4*)(xv + 4 * g));
+    for (u32 g = 0; g < 8; g++) l[g] = leaf4(w + 32 * q + 4 * g, xv[8 * q + g]);
     s[q] = ((l[0] + l[1]) + (l[2] + l[3])) + ((l[4] + l[5]) + (l[6] + l[7]));
   }
 #pragma unroll
@@ -38,7 +37,6 @@ DEV float tree_row_lane(const float* w, const float* __restrict__ x, u32 c0base)
   return s[0];
 }
 
-template <u32 NSP>
 DEV void span_any(u32 fm, const u8* rp, u32 c0, float* w) {
   switch (fm) {
     case FM_F32: Span<FM_F32>::w(rp, c0, w); break;
@@ -48,34 +46,40 @@ DEV void span_any(u32 fm, const u8* rp, u32 c0, float* w) {
   }
 }
 
+#define TREE_RPW 2  // rows a wave: the lane's x span is loaded once for them
+
 // every tree row of the layer in one launch (router, shared gate logit, shared gate, shared up):
-// one wave a row, blockDim 256 (4 rows), grid (ceil(rows / 4), ceil(T / tch))
+// a wave takes TREE_RPW consecutive rows (of the concatenated segments), lane L the contiguous
+// leaves [L S, L S + S); blockDim 64, grid (ceil(rows / TREE_RPW), T)
 template <u32 NSP>
-__global__ void __launch_bounds__(256) k_tree_rows(TreeArgs a) {
-  u32 row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const u32 L = threadIdx.x & 63;
-  u32 sgi = 0;
-  while (sgi < a.nseg && row >= a.seg[sgi].rows) { row -= a.seg[sgi].rows; sgi++; }
-  if (sgi >= a.nseg) return;
-  const TreeSeg sg = a.seg[sgi];
+DEV void tree_body(const TreeArgs& a, u32 bx, u32 t, u32 L) {
   const u32 c0 = 32 * NSP * L;
   const bool live = c0 < a.cols;  // pad leaves past cols count +0
-  float w[32 * NSP];
-  const u8* rp = sg.W + (u64)row * sg.rb;
+  float4 xv[8 * NSP];
+  const float* x = a.x + (u64)t * a.xstride;
 #pragma unroll
-  for (u32 q = 0; q < NSP; q++) {
-    if (live) span_any<NSP>(sg.fm, rp, c0 + 32 * q, w + 32 * q);
-    else
+  for (u32 q = 0; q < 8 * NSP; q++) xv[q] = live ? ((const float4*)(x + c0))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (u32 k = 0; k < TREE_RPW; k++) {
+    u32 row = bx * TREE_RPW + k, sgi = 0;
+    while (sgi < a.nseg && row >= a.seg[sgi].rows) { row -= a.seg[sgi].rows; sgi++; }
+    if (sgi >= a.nseg) return;
+    const TreeSeg& sg = a.seg[sgi];
+    float w[32 * NSP];
 #pragma unroll
-      for (u32 i = 0; i < 32; i++) w[32 * q + i] = 0.0f;
-  }
-  const u32 t0 = blockIdx.y * a.tch, t1 = min(a.T, t0 + a.tch);
-  for (u32 t = t0; t < t1; t++) {
-    float v = 0.0f;
-    if (live) v = tree_row_lane<NSP>(w, a.x + (u64)t * a.xstride, c0);  // else every leaf is a +0 pad
+    for (u32 q = 0; q < NSP; q++) {
+      if (live) span_any(sg.fm, sg.W + (u64)row * sg.rb, c0 + 32 * q, w + 32 * q);
+      else
+#pragma unroll
+        for (u32 i = 0; i < 32; i++) w[32 * q + i] = 0.0f;
+    }
+    float v = live ? tree_row_lane<NSP>(w, xv) : 0.0f;  // a dead lane's leaves are all +0 pads
     v = tree64_asc(v);
     if (L == 0) sg.out[(u64)t * sg.ostride + row] = v;
   }
+}
+template <u32 NSP>
+__global__ void __launch_bounds__(64) k_tree_rows(TreeArgs a) {
+  tree_body<NSP>(a, blockIdx.x, blockIdx.y, threadIdx.x);
 }
 
 // ---------------------------------------------------------------- top-k (llb_moe_topk)
@@ -106,8 +110,7 @@ DEV void wave_amax(float& bv, u32& bi) {
 // the 1024-thread block's order (thread t = expert t: each 32-expert group by the xor tree 16 .. 1,
 // then the group sums in order); p = v (1 / sum); the k largest p, ties to the lower index;
 // wt_j = p / max(sum of the k p in rank order, 2^-14); sgo = sigmoid(sg)
-__global__ void __launch_bounds__(64) k_topk(TopkArgs a) {
-  const u32 t = blockIdx.x, L = threadIdx.x;
+DEV void topk_body(const TopkArgs& a, u32 t, u32 L) {
   const float* lg = a.lg + (u64)t * a.lstride;
   const u32 ni = (a.ne + 63) / 64;
   float p[16];
@@ -161,6 +164,7 @@ __global__ void __launch_bounds__(64) k_topk(TopkArgs a) {
     a.sgo[t] = 1.0f / (1.0f + exp_f(-sg));
   }
 }
+__global__ void __launch_bounds__(64) k_topk(TopkArgs a) { topk_body(a, blockIdx.x, threadIdx.x); }
 
 // ---------------------------------------------------------------- stride rows (experts)
 //
@@ -200,37 +204,57 @@ DEV float stride_sum(const float* lv, u32 ng, u32 v) {
 }
 
 // gate + up + SwiGLU (llb_moe_gu): a block takes np (gate, up) row pairs of one slot, 2 np rows of
-// dm columns. Leaves [2 np][dm / 4] in LDS; gate rows even, up rows odd.
+// dm columns. x goes to LDS once; thread t owns span t % ns and walks rows t / ns, t / ns + 256 / ns,
+// ... (gate rows even, up rows odd), so its slice of x is read once. Leaves [2 np][dm / 4] in LDS.
 template <u32 FG, u32 FU>
-__global__ void __launch_bounds__(256) k_gu_exact(GuArgs a, u32 np) {
-  extern __shared__ float lv[];
-  const u32 task0 = blockIdx.x * np, slot = task0 / a.ef, r0 = task0 % a.ef;
+DEV void gu_body(const GuArgs& a, u32 np, u32 bx, float* sm) {
+  float* xs = sm;              // [dm]
+  float* lv = sm + a.dm;       // [2 np][dm / 4]
+  const u32 task0 = bx * np, slot = task0 / a.ef, r0 = task0 % a.ef;
   const u32 t = slot / a.nk;
   const float* x = a.h2 + (u64)t * a.dm;
+  for (u32 i = threadIdx.x; i < a.dm / 4; i += 256) ((float4*)xs)[i] = ((const float4*)x)[i];
   const u64 e = a.ids[slot];
-  const u32 ns = a.dm / 32, ng = a.dm / 4, items = 2 * np * ns;
-  for (u32 it = threadIdx.x; it < items; it += 256) {
-    const u32 rr = it / ns, sp = it % ns, row = r0 + (rr >> 1);
-    float l[8];
-    if ((rr & 1) == 0) span_leaves<FG>(a.G + e * a.es + row * a.rbg, 32 * sp, x, l);
-    else span_leaves<FU>(a.U + e * a.es + row * a.rbu, 32 * sp, x, l);
-    store_leaves(lv + rr * ng + 8 * sp, l);
+  const u32 ns = a.dm / 32, ng = a.dm / 4, nr = 2 * np;
+  __syncthreads();
+  const bool walk = 256 % ns == 0;  // fixed span column a thread: x read once for its rows
+  for (u32 it = threadIdx.x; it < (walk ? ns * (256 / ns) : nr * ns); it += 256) {
+    const u32 c = it % ns;
+    float4 xv[8];
+#pragma unroll
+    for (u32 g = 0; g < 8; g++) xv[g] = ((const float4*)(xs + 32 * c))[g];
+    for (u32 rr = it / ns; rr < nr; rr += walk ? 256 / ns : nr) {
+      const u32 row = r0 + (rr >> 1);
+      float w[32], l[8];
+      if ((rr & 1) == 0) Span<FG>::w(a.G + e * a.es + row * a.rbg, 32 * c, w);
+      else Span<FU>::w(a.U + e * a.es + row * a.rbu, 32 * c, w);
+#pragma unroll
+      for (u32 g = 0; g < 8; g++) l[g] = leaf4(w + 4 * g, xv[g]);
+      store_leaves(lv + rr * ng + 8 * c, l);
+    }
   }
   __syncthreads();
   const u32 rr = threadIdx.x >> 5, v = threadIdx.x & 31;
-  float s = 0.0f;
-  if (rr < 2 * np) s = stride_sum(lv + rr * ng, ng, v);
-  const float u = xpeer32(s);  // the up row sits in the other half of the wave
-  if (rr < 2 * np && (rr & 1) == 0 && v == 0) a.act[(u64)slot * a.ef + r0 + (rr >> 1)] = silu_mul(s, u);
+  for (u32 rb = 0; rb < nr; rb += 8) {
+    const u32 r = rb + rr;
+    float s = 0.0f;
+    if (r < nr) s = stride_sum(lv + r * ng, ng, v);
+    const float u = xpeer32(s);  // the up row sits in the other half of the wave
+    if (r < nr && (r & 1) == 0 && v == 0) a.act[(u64)slot * a.ef + r0 + (r >> 1)] = silu_mul(s, u);
+  }
+}
+template <u32 FG, u32 FU>
+__global__ void __launch_bounds__(256) k_gu_exact(GuArgs a, u32 np) {
+  extern __shared__ float sm[];
+  gu_body<FG, FU>(a, np, blockIdx.x, sm);
 }
 
 // down + rank-order combine + gated shared expert + residual (llb_moe_dn): rw rows of one token a
 // block; task j < nk is routed expert ids[j]'s row against act_j, j = nk the shared expert's down
 // row against sa (computed here from the shared gate / up logits)
 template <u32 FD, u32 FS>
-__global__ void __launch_bounds__(256) k_dn_exact(DnArgs a) {
-  extern __shared__ float sm[];
-  const u32 t = blockIdx.y, nt = a.nk + (FS ? 1u : 0u);
+DEV void dn_body(const DnArgs& a, u32 bx, u32 t, float* sm) {
+  const u32 nt = a.nk + (FS ? 1u : 0u);
   const u32 nge = a.ef / 4, ngs = a.sf / 4, per_row = a.nk * nge + (FS ? ngs : 0u);
   float* lv = sm;                                  // [rw][nk ef / 4 + sf / 4]
   float* sa = sm + a.rw * per_row;                 // [sf]
@@ -241,20 +265,25 @@ __global__ void __launch_bounds__(256) k_dn_exact(DnArgs a) {
     __syncthreads();
   }
   const float* act = a.act + (u64)t * a.nk * a.ef;
-  const u32 nse = a.ef / 32, nss = a.sf / 32, spr = a.nk * nse + (FS ? nss : 0u);
-  const u32 items = a.rw * spr;
-  for (u32 it = threadIdx.x; it < items; it += 256) {
-    const u32 rl = it / spr, q = it % spr, r = min(blockIdx.x * a.rw + rl, a.dm - 1);
-    float l[8];
-    if (q < a.nk * nse) {
-      const u32 j = q / nse, sp = q % nse;
-      const u64 e = a.ids[(u64)t * a.nk + j];
-      span_leaves<FD>(a.D + (e * a.dm + r) * a.rbd, 32 * sp, act + (u64)j * a.ef, l);
+  // column q = one 32-column span of one task: q < nk ef / 32 routed (task q / (ef / 32)), then
+  // the shared expert's; a thread loads its x slice once and walks the block's rw rows
+  const u32 nse = a.ef / 32, nss = a.sf / 32, ncol = a.nk * nse + (FS ? nss : 0u);
+  for (u32 q = threadIdx.x; q < ncol; q += 256) {
+    const bool routed = q < a.nk * nse;
+    const u32 j = routed ? q / nse : a.nk, sp = routed ? q % nse : q - a.nk * nse;
+    const float* xsrc = routed ? act + (u64)j * a.ef + 32 * sp : sa + 32 * sp;
+    float4 xv[8];
+#pragma unroll
+    for (u32 g = 0; g < 8; g++) xv[g] = ((const float4*)xsrc)[g];
+    const u64 e = routed ? a.ids[(u64)t * a.nk + j] : 0;
+    for (u32 rl = 0; rl < a.rw; rl++) {
+      const u32 r = min(bx * a.rw + rl, a.dm - 1);
+      float w[32], l[8];
+      if (routed) Span<FD>::w(a.D + (e * a.dm + r) * a.rbd, 32 * sp, w);
+      else Span<FS ? FS : FM_Q4_K>::w(a.SD + (u64)r * a.rbs, 32 * sp, w);
+#pragma unroll
+      for (u32 g = 0; g < 8; g++) l[g] = leaf4(w + 4 * g, xv[g]);
       store_leaves(lv + rl * per_row + j * nge + 8 * sp, l);
-    } else {
-      const u32 sp = q - a.nk * nse;
-      span_leaves<FS ? FS : FM_Q4_K>(a.SD + (u64)r * a.rbs, 32 * sp, sa, l);
-      store_leaves(lv + rl * per_row + a.nk * nge + 8 * sp, l);
     }
   }
   __syncthreads();
@@ -264,16 +293,15 @@ __global__ void __launch_bounds__(256) k_dn_exact(DnArgs a) {
     float s = 0.0f;
     if (q < sums) {
       const u32 rl = k / nt, j = k % nt;
-      const float* base = lv + rl * per_row + j * nge;
-      s = stride_sum(base, j < a.nk ? nge : ngs, v);
+      s = stride_sum(lv + rl * per_row + j * nge, j < a.nk ? nge : ngs, v);
     } else {
-      s = stride_sum(lv, 0, v);  // keeps the shuffles of a partial wave uniform
+      s = stride_sum(lv, 0, v);  // keeps a partial wave's cross-lane steps uniform
     }
     if (q < sums && v == 0) part[k] = s;
   }
   __syncthreads();
   if (threadIdx.x < a.rw) {
-    const u32 r = blockIdx.x * a.rw + threadIdx.x;
+    const u32 r = bx * a.rw + threadIdx.x;
     if (r < a.dm) {
       const float* wt = a.wt + (u64)t * a.nk;
       const float* pr = part + threadIdx.x * nt;
@@ -282,6 +310,92 @@ __global__ void __launch_bounds__(256) k_dn_exact(DnArgs a) {
       const float res = a.x1 ? a.x1[(u64)t * a.dm + r] : 0.0f;
       a.y[(u64)t * a.dm + r] = FS ? (mo + pr[a.nk] * a.sgo[t]) + res : mo + res;
     }
+  }
+}
+template <u32 FD, u32 FS>
+__global__ void __launch_bounds__(256) k_dn_exact(DnArgs a) {
+  extern __shared__ float sm[];
+  dn_body<FD, FS>(a, blockIdx.x, blockIdx.y, sm);
+}
+
+// ---------------------------------------------------------------- the fused decode layer
+//
+// One persistent launch runs a whole layer. Blocks take work items from a ticket counter in a
+// fixed order -- tree rows (router, shared gate logit, shared gate / up), then one top-k item a
+// token, then gate / up items, then down items -- and an item waits, where it must, for every item
+// of the phase before it (a completion counter). Tickets are handed out in order, so an item only
+// ever waits for items that running blocks already hold: no deadlock whatever the grid size. A
+// wait is bounded (a wall-clock limit); past it the block records an error and carries on, so the
+// grid always drains. The last block out zeroes the counters for the next launch.
+//
+// Cross-block visibility: a finished item's stores are released (agent-scope fence in every wave,
+// then the block barrier) before its counter increment; a waiting block acquires (agent-scope
+// fence in every wave) after it sees the count.
+
+// A counter is read with a read-modify-write atomic, like the increments (L2 atomics), not with a
+// cache-bypassing load, which on another XCD need not see them. The compiler turns an idempotent
+// RMW (add 0) back into a load, so the read is a compare-exchange against a value the counter
+// never holds: it fails and returns the current count, writing nothing.
+DEV u32 ctr_read(u32* p) {
+  u32 v = 0xFFFFFFFFu;
+  __hip_atomic_compare_exchange_strong(p, &v, 0xFFFFFFFFu, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return v;
+}
+
+// wait until *ctr >= target, at most `limit` ticks of the 100 MHz wall clock
+DEV void phase_wait(u32* ctr, u32 target, u32* err, u32 limit) {
+  if (threadIdx.x == 0) {
+    const u64 t0 = __builtin_amdgcn_s_memrealtime();
+    while (ctr_read(ctr) < target) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > limit) {
+        __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
+  __syncthreads();
+  __threadfence();
+}
+DEV void item_done(u32* ctr) {
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <u32 FG, u32 FD, u32 FS, u32 NSP>
+__global__ void __launch_bounds__(256) k_fused(FusedArgs f) {
+  extern __shared__ float sm[];
+  __shared__ u32 ticket;
+  u32* c = f.ctr;  // [0] tickets, [1] tree done, [2] top-k done, [3] gate/up done, [4] blocks out, [5] error
+  const u32 w = threadIdx.x >> 6, L = threadIdx.x & 63;
+  const u32 nK = f.T, e1 = f.nR, e2 = e1 + nK, e3 = e2 + f.nG, total = e3 + f.nD;
+  for (;;) {
+    if (threadIdx.x == 0) ticket = __hip_atomic_fetch_add(&c[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const u32 it = ticket;
+    __syncthreads();
+    if (it >= total) break;
+    if (it < e1) {
+      const u32 t = it / f.rpt, sub = it % f.rpt;
+      tree_body<NSP>(f.tr, 4 * sub + w, t, L);
+      item_done(&c[1]);
+    } else if (it < e2) {
+      phase_wait(&c[1], f.nR, &c[5], f.spin);
+      if (w == 0) topk_body(f.tk, it - e1, L);
+      item_done(&c[2]);
+    } else if (it < e3) {
+      phase_wait(&c[2], nK, &c[5], f.spin);
+      gu_body<FG, FG>(f.gu, f.np, it - e2, sm);
+      item_done(&c[3]);
+    } else {
+      phase_wait(&c[3], f.nG, &c[5], f.spin);
+      const u32 k = it - e3;
+      dn_body<FD, FS>(f.dn, k % f.dpt, k / f.dpt, sm);
+    }
+  }
+  if (threadIdx.x == 0 && __hip_atomic_fetch_add(&c[4], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1) {
+    for (u32 i = 0; i < 5; i++) __hip_atomic_exchange(&c[i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -309,10 +423,10 @@ int launch_tree_rows(const TreeArgs& a, u32 nsp, hipStream_t st) {
   u32 rows = 0;
   for (u32 i = 0; i < a.nseg; i++) rows += a.seg[i].rows;
   if (rows == 0) return 0;
-  dim3 grid((rows + 3) / 4, (a.T + a.tch - 1) / a.tch);
-  if (nsp == 1) { hipLaunchKernelGGL((k_tree_rows<1>), grid, dim3(256), 0, st, a); return 0; }
-  if (nsp == 2) { hipLaunchKernelGGL((k_tree_rows<2>), grid, dim3(256), 0, st, a); return 0; }
-  if (nsp == 4) { hipLaunchKernelGGL((k_tree_rows<4>), grid, dim3(256), 0, st, a); return 0; }
+  dim3 grid((rows + TREE_RPW - 1) / TREE_RPW, a.T);
+  if (nsp == 1) { hipLaunchKernelGGL((k_tree_rows<1>), grid, dim3(64), 0, st, a); return 0; }
+  if (nsp == 2) { hipLaunchKernelGGL((k_tree_rows<2>), grid, dim3(64), 0, st, a); return 0; }
+  if (nsp == 4) { hipLaunchKernelGGL((k_tree_rows<4>), grid, dim3(64), 0, st, a); return 0; }
   return -1;
 }
 
@@ -323,9 +437,9 @@ int launch_topk(const TopkArgs& a, u32 T, hipStream_t st) {
 
 int launch_gu_exact(const GuArgs& a, u32 fg, u32 fu, u32 nslots, hipStream_t st) {
   if (fg != fu) return -1;
-  const u32 np = a.dm >= 4096 ? 1u : 2u;  // 2 np rows of dm / 32 spans: about one span a thread
+  const u32 np = 4;  // 8 rows a block: at dm 2048 each thread decodes one span of 2 rows
   dim3 grid(nslots * a.ef / np);
-  const size_t sm = (size_t)2 * np * (a.dm / 4) * 4;
+  const size_t sm = ((size_t)a.dm + (size_t)2 * np * (a.dm / 4)) * 4;
 #define GU_L(F) \
   if (fg == F) { hipLaunchKernelGGL((k_gu_exact<F, F>), grid, dim3(256), sm, st, a, np); return 0; }
   FM_CASES(GU_L)
@@ -333,11 +447,10 @@ int launch_gu_exact(const GuArgs& a, u32 fg, u32 fu, u32 nslots, hipStream_t st)
   return -1;
 }
 
-// rows a down block takes: about 512 span items (two a thread), at least one row
+// rows a down block takes: each thread's x slice serves rw rows
 u32 dn_rows(u32 nk, u32 ef, u32 sf) {
-  const u32 spr = nk * (ef / 32) + sf / 32;
-  u32 rw = 512 / spr;
-  return rw < 1 ? 1 : rw > 8 ? 8 : rw;
+  (void)nk; (void)ef; (void)sf;
+  return 4;
 }
 
 int launch_dn_exact(const DnArgs& a, u32 fd, u32 fs, u32 T, hipStream_t st) {
@@ -351,6 +464,36 @@ int launch_dn_exact(const DnArgs& a, u32 fd, u32 fs, u32 T, hipStream_t st) {
 #undef DN_FS
 #undef DN_L
   return -1;
+}
+
+// the fused path's format combinations (others take the four-launch path)
+#define FUSED_CASES(X) \
+  X(FM_Q8_0, FM_Q8_0, 0u) X(FM_Q4_K, FM_Q6_K, FM_Q6_K) X(FM_Q4_K, FM_Q6_K, 0u) X(FM_Q4_K, FM_Q4_K, 0u) \
+  X(FM_Q4_K, FM_Q4_K, FM_Q6_K) X(FM_Q6_K, FM_Q6_K, FM_Q6_K) X(FM_Q5_K, FM_Q5_K, FM_Q4_K) X(FM_Q6_K, FM_Q8_0, FM_Q6_K)
+
+size_t fused_lds(const FusedArgs& f) {
+  const size_t gu = ((size_t)f.gu.dm + (size_t)2 * f.np * (f.gu.dm / 4)) * 4;
+  const u32 nt = f.dn.nk + (f.dn.sf ? 1u : 0u);
+  const size_t dn = ((size_t)f.dn.rw * (f.dn.nk * f.dn.ef / 4 + f.dn.sf / 4) + f.dn.sf + f.dn.rw * nt) * 4;
+  return gu > dn ? gu : dn;
+}
+
+int launch_fused(const FusedArgs& f, u32 fg, u32 fd, u32 fs, u32 nsp, u32 grid, hipStream_t st) {
+  const size_t sm = fused_lds(f);
+#define FU_L(FG, FD, FS) \
+  if (fg == FG && fd == FD && fs == FS) { \
+    if (nsp == 1) { hipLaunchKernelGGL((k_fused<FG, FD, FS, 1>), dim3(grid), dim3(256), sm, st, f); return 0; } \
+    if (nsp == 2) { hipLaunchKernelGGL((k_fused<FG, FD, FS, 2>), dim3(grid), dim3(256), sm, st, f); return 0; } \
+  }
+  FUSED_CASES(FU_L)
+#undef FU_L
+  return -1;
+}
+bool fused_supported(u32 fg, u32 fd, u32 fs, u32 nsp) {
+#define FU_S(FG, FD, FS) if (fg == FG && fd == FD && fs == FS && (nsp == 1 || nsp == 2)) return true;
+  FUSED_CASES(FU_S)
+#undef FU_S
+  return false;
 }
 
 int launch_dequant(u32 fm, const u8* W, u64 rb, u32 rows, u32 cols, float* out, hipStream_t st) {

@@ -53,6 +53,20 @@ struct DnArgs {
   float* y;
 };
 
+struct FusedArgs {
+  TreeArgs tr;
+  TopkArgs tk;
+  GuArgs gu;
+  DnArgs dn;
+  uint32_t T, nR, nG, nD;
+  uint32_t rpt;  // tree items a token (4 waves x 2 rows an item)
+  uint32_t dpt;  // down items a token
+  uint32_t np;   // gate / up row pairs an item
+  uint32_t spin; // 100 MHz ticks a wait may take before it records an error
+  uint32_t* ctr; // 6 counters in the scratch, zero between launches
+};
+int launch_fused(const FusedArgs& f, uint32_t fg, uint32_t fd, uint32_t fs, uint32_t nsp, uint32_t grid, hipStream_t st);
+bool fused_supported(uint32_t fg, uint32_t fd, uint32_t fs, uint32_t nsp);
 int launch_tree_rows(const TreeArgs& a, uint32_t nsp, hipStream_t st);
 uint32_t dn_rows(uint32_t nk, uint32_t ef, uint32_t sf);
 int launch_topk(const TopkArgs& a, uint32_t T, hipStream_t st);

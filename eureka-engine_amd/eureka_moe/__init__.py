@@ -60,6 +60,8 @@ _SIGS = {
     "llb_moe_hip_scratch_bytes": (C.c_size_t, [C.POINTER(MoeLayer), C.c_uint32, C.c_int]),
     "llb_moe_hip_forward": (C.c_int, [C.POINTER(MoeLayer), C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64,
                                       C.c_uint64, C.c_uint64, C.c_size_t, C.c_int]),
+    "llb_moe_hip_set_fused": (C.c_int, [C.c_int]),
+    "llb_moe_hip_status": (C.c_int, [C.c_uint64, C.POINTER(MoeLayer), C.c_uint32]),
     "llb_moe_hip_topk": (C.c_int, [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64,
                                    C.c_uint64, C.c_uint64]),
     "llb_moe_hip_group": (C.c_int, [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64,
@@ -269,6 +271,10 @@ class Runner:
         self.dev.check(self.dev.lib.llb_moe_hip_forward(C.byref(layer.desc), self.T, self.h2, self.x1 if residual else 0,
                                                         self.y, self.ids, self.wt, self.scratch, self.scratch_bytes,
                                                         self.tier))
+
+    def status(self, layer):
+        """raises if a fused launch on this runner's scratch had a phase wait time out."""
+        self.dev.check(self.dev.lib.llb_moe_hip_status(self.scratch, C.byref(layer.desc), self.T))
 
     def outputs(self):
         s = self.shape

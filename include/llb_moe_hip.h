@@ -91,6 +91,14 @@ size_t llb_moe_hip_scratch_bytes(const llb_moe_layer* L, uint32_t T, int tier);
 int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dptr x1, llb_dptr y, llb_dptr ids,
                         llb_dptr wt, llb_dptr scratch, size_t scratch_bytes, int tier);
 
+/* The exact tier at T <= 8 runs a layer as one persistent launch (the "fused" path; the four-launch
+ * sequence otherwise). The fused path keeps 6 counters in the scratch, which must be zero before
+ * its first use (llb_hip_alloc_zero gives that) and which every launch leaves zero. on = 0 forces
+ * the four-launch path (same bits). status returns LLB_HIP_EDEVICE (and clears it) when a fused
+ * launch on that scratch had a bounded wait time out. No counterpart in the reference. */
+int llb_moe_hip_set_fused(int on);
+int llb_moe_hip_status(llb_dptr scratch, const llb_moe_layer* L, uint32_t T);
+
 /* ---- kernel-level entry points ---- */
 /* llb_moe_topk block 0 (tools/payload-moeany.patch:311-470) for T tokens: lg [T][lstride] (ne logits,
  * then the shared gate's at index ne when has_sg) -> ids, wt [T][nk], sgo [T] */

@@ -46,12 +46,20 @@ def test_gauss_bit_exact(dev):
     dev.free(p)
 
 
-def _exact_case(dev, shape, seed, T, residual=True):
-    _say("exact", vars(shape), "seed", seed, "T", T)
+FUSED_SKIP = ("the fused one-launch layer hung on the GPU twice and its cause is not shown; the path is off "
+              "(llb_moe_hip_set_fused defaults to 0) until it is")
+
+
+def _exact_case(dev, shape, seed, T, residual=True, fused=False):
+    _say("exact", vars(shape), "seed", seed, "T", T, "fused" if fused else "four launches")
+    dev.check(dev.lib.llb_moe_hip_set_fused(1 if fused else 0))
     layer = em.Layer(dev, shape, seed=seed)
     run = em.Runner(dev, shape, T)
     run.gen_inputs(seed)
     run.forward(layer, residual=residual)
+    run.forward(layer, residual=residual)  # twice: the fused path's counters must come back to zero
+    run.status(layer)
+    dev.check(dev.lib.llb_moe_hip_set_fused(0))
     y, ids, wt = run.outputs()
     run.free()
     layer.free()
@@ -70,18 +78,21 @@ SMALL = [
 ]
 
 
+@pytest.mark.parametrize("fused", [pytest.param(True, marks=pytest.mark.skip(reason=FUSED_SKIP)), False])
 @pytest.mark.parametrize("si", range(len(SMALL)))
-def test_exact_small_bit_exact(dev, si):
-    y, ids, wt, yr, idr, wtr, _, _ = _exact_case(dev, SMALL[si], seed=100 + si, T=3)
+def test_exact_small_bit_exact(dev, si, fused):
+    y, ids, wt, yr, idr, wtr, _, _ = _exact_case(dev, SMALL[si], seed=100 + si, T=3, fused=fused)
     assert np.array_equal(ids, idr)
     assert np.array_equal(wt.view(np.uint32), wtr.view(np.uint32))
     assert np.array_equal(y.view(np.uint32), yr.view(np.uint32)), float(np.abs(y - yr).max())
 
 
-@pytest.mark.parametrize("name,seed", [("c1", 0), ("c2", 0), ("c2", 1), ("c1k", 3)])
-def test_exact_configs_bit_exact(dev, name, seed):
+@pytest.mark.parametrize("name,seed,fused", [("c1", 0, False), ("c2", 0, False), ("c2", 1, False), ("c1k", 3, False),
+                                             ("c5", 0, False),
+                                             pytest.param("c2", 5, True, marks=pytest.mark.skip(reason=FUSED_SKIP))])
+def test_exact_configs_bit_exact(dev, name, seed, fused):
     shape = em.SHAPES[name]
-    y, ids, wt, yr, idr, wtr, hl, h2 = _exact_case(dev, shape, seed, T=1, residual=False)
+    y, ids, wt, yr, idr, wtr, hl, h2 = _exact_case(dev, shape, seed, T=1, residual=False, fused=fused)
     assert np.array_equal(ids, idr)
     assert np.array_equal(wt.view(np.uint32), wtr.view(np.uint32))
     assert np.array_equal(y.view(np.uint32), yr.view(np.uint32)), float(np.abs(y - yr).max())
