@@ -236,16 +236,38 @@ static ExactScratch exact_layout(const llb_moe_layer* L, uint32_t T) {
   return s;
 }
 
+struct GemmScratch {
+  size_t x16, off, xmap, inv, tiles, ntiles, act, out, sact, shd, total;
+};
+static GemmScratch gemm_layout(const llb_moe_layer* L, uint32_t T) {
+  GemmScratch g;
+  const size_t n = (size_t)T * L->nk;
+  size_t o = 0;
+  g.x16 = o; o += al((size_t)T * L->dm * 2);
+  g.off = o; o += al(((size_t)L->ne + 1) * 4);
+  g.xmap = o; o += al(n * 4);
+  g.inv = o; o += al(n * 4);
+  g.tiles = o; o += al((n / gemm_bm() + L->ne + 1) * 4);
+  g.ntiles = o; o += al(4);
+  g.act = o; o += al(n * L->ef * 2);
+  g.out = o; o += al(n * L->dm * 4);
+  g.sact = o; o += al((size_t)T * L->sf * 2 + 4);
+  g.shd = o; o += al((size_t)T * L->dm * 4);
+  g.total = o;
+  return g;
+}
+
 size_t llb_moe_hip_scratch_bytes(const llb_moe_layer* L, uint32_t T, int tier) {
   if (!L || !T) return 0;
   const size_t a = exact_layout(L, T).total;
   if (tier == LLB_MOE_Q8) return a + moe_q8_scratch(L, T);
+  if (tier == LLB_MOE_F16) return a + gemm_layout(L, T).total;
   return a;
 }
 
 // router + shared gate logit + shared gate / up (the tree rows), then top-k and sa
 static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* ids, float* wt, uint8_t* sc,
-                 const ExactScratch& s) {
+                 const ExactScratch& s, bool shared_rows = true) {
   float* lg = (float*)(sc + s.lg);
   float* gsu = (float*)(sc + s.gsu);
   TreeArgs a{};
@@ -259,7 +281,7 @@ static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* 
   a.seg[1] = TreeSeg{dp<uint8_t>(L->shgate), LLB_FM_F32, (uint64_t)L->dm * 4, L->sf ? 1u : 0u, lg + L->ne, L->ne + 1};
   a.seg[2] = TreeSeg{dp<uint8_t>(L->SG), L->fsg, row_bytes(L->fsg, L->dm), L->sf, gsu, 2 * L->sf};
   a.seg[3] = TreeSeg{dp<uint8_t>(L->SU), L->fsu, row_bytes(L->fsu, L->dm), L->sf, gsu + L->sf, 2 * L->sf};
-  a.nseg = 4;
+  a.nseg = shared_rows ? 4 : 2;
   int rc;
   stage_begin(ST_ROUTE);
   if ((rc = launched(launch_tree_rows(a, ns, g_stream), "router + shared gate / up"))) return rc;
@@ -282,6 +304,90 @@ static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* 
 
 static int fused_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const float* x1, float* y, uint32_t* ids,
                          float* wt, uint8_t* sc, const ExactScratch& s);
+
+// the grouped-GEMM tier: exact routing, the dispatch permutation, expert GEMMs on MFMA, combine
+static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const float* x1, float* y, uint32_t* ids,
+                        float* wt, uint8_t* sc, const ExactScratch& s) {
+  const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
+  if (fg != fu) return fail(LLB_HIP_EINVAL, "f16 tier: gate and up in one format");
+  if (L->sf && L->fsg != L->fsu) return fail(LLB_HIP_EINVAL, "f16 tier: shared gate and up in one format");
+  if (L->dm % 128 || L->ef % 128 || L->sf % 128 || L->ne >= 65536)
+    return fail(LLB_HIP_EINVAL, "f16 tier: dm, ef, sf multiples of 128");
+  const GemmScratch gs = gemm_layout(L, T);
+  uint8_t* gb = sc + s.total;
+  int rc;
+  if ((rc = route(L, T, h2, ids, wt, sc, s, false))) return rc;
+  const uint32_t n = T * L->nk;
+  uint32_t* off = (uint32_t*)(gb + gs.off);
+  uint32_t* xmap = (uint32_t*)(gb + gs.xmap);
+  uint32_t* inv = (uint32_t*)(gb + gs.inv);
+  uint32_t* tiles = (uint32_t*)(gb + gs.tiles);
+  uint32_t* ntiles = (uint32_t*)(gb + gs.ntiles);
+  _Float16* x16 = (_Float16*)(gb + gs.x16);
+  stage_begin(ST_Q8X);
+  if ((rc = launched(launch_group(ids, n, L->nk, L->ne, off, xmap, inv, nullptr, g_stream), "group"))) return rc;
+  if ((rc = launched(launch_tiles(off, L->ne, tiles, ntiles, g_stream), "tiles"))) return rc;
+  if ((rc = launched(launch_to_f16(h2, x16, (uint64_t)T * L->dm, g_stream), "to f16"))) return rc;
+  stage_end(ST_Q8X);
+  const uint64_t rbg = row_bytes(fg, L->dm), rbd = row_bytes(fd, L->ef);
+  const uint32_t maxt = n / gemm_bm() + L->ne + 1;  // >= sum over experts of ceil(M_e / BM)
+  GemmArgs g{};
+  g.W0 = dp<uint8_t>(L->G);
+  g.W1 = fz ? g.W0 + (uint64_t)L->ef * rbg : dp<uint8_t>(L->U);
+  g.es = (uint64_t)(fz ? 2 : 1) * L->ef * rbg;
+  g.rb = rbg;
+  g.K = L->dm;
+  g.N = L->ef;
+  g.A = x16;
+  g.xmap = xmap;
+  g.off = off;
+  g.tiles = tiles;
+  g.ntiles = ntiles;
+  g.out = gb + gs.act;
+  stage_begin(ST_GU);
+  if ((rc = launched(launch_moe_gemm(g, fg, 0, maxt, g_stream), "expert gate/up GEMM"))) return rc;
+  stage_end(ST_GU);
+  GemmArgs d = g;
+  d.W0 = dp<uint8_t>(L->D);
+  d.W1 = nullptr;
+  d.es = (uint64_t)L->dm * rbd;
+  d.rb = rbd;
+  d.K = L->ef;
+  d.N = L->dm;
+  d.A = (const _Float16*)(gb + gs.act);
+  d.xmap = nullptr;
+  d.out = gb + gs.out;
+  stage_begin(ST_DN);
+  if ((rc = launched(launch_moe_gemm(d, fd, 1, maxt, g_stream), "expert down GEMM"))) return rc;
+  stage_end(ST_DN);
+  const float* shd = nullptr;
+  if (L->sf) {
+    const uint32_t mt = (T + gemm_bm() - 1) / gemm_bm();
+    GemmArgs sg{};
+    sg.W0 = dp<uint8_t>(L->SG);
+    sg.W1 = dp<uint8_t>(L->SU);
+    sg.rb = row_bytes(L->fsg, L->dm);
+    sg.K = L->dm;
+    sg.N = L->sf;
+    sg.M = T;
+    sg.A = x16;
+    sg.out = gb + gs.sact;
+    if ((rc = launched(launch_moe_gemm(sg, L->fsg, 0, mt, g_stream), "shared gate/up GEMM"))) return rc;
+    GemmArgs sd{};
+    sd.W0 = dp<uint8_t>(L->SD);
+    sd.rb = row_bytes(L->fsd, L->sf);
+    sd.K = L->sf;
+    sd.N = L->dm;
+    sd.M = T;
+    sd.A = (const _Float16*)(gb + gs.sact);
+    sd.out = gb + gs.shd;
+    if ((rc = launched(launch_moe_gemm(sd, L->fsd, 1, mt, g_stream), "shared down GEMM"))) return rc;
+    shd = (const float*)(gb + gs.shd);
+  }
+  return launched(launch_combine((const float*)(gb + gs.out), inv, wt, L->nk, shd, (const float*)(sc + s.sgo), x1, y,
+                                 L->dm, T, g_stream),
+                  "combine");
+}
 
 // the fused one-launch layer (exact tier, small T) on by default; 0 forces the four-launch path
 static int g_fused = 0;
@@ -311,7 +417,7 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
   if (rc) return rc;
   if (T == 0) return 0;
   if (!h2 || !y || !ids || !wt || !scratch) return fail(LLB_HIP_EINVAL, "null buffer");
-  if (tier != LLB_MOE_EXACT && tier != LLB_MOE_Q8) return fail(LLB_HIP_EINVAL, "unknown tier %d", tier);
+  if (tier != LLB_MOE_EXACT && tier != LLB_MOE_Q8 && tier != LLB_MOE_F16) return fail(LLB_HIP_EINVAL, "unknown tier %d", tier);
   if (scratch_bytes < llb_moe_hip_scratch_bytes(L, T, tier))
     return fail(LLB_HIP_ESCRATCH, "scratch %zu < %zu bytes", scratch_bytes, llb_moe_hip_scratch_bytes(L, T, tier));
   uint8_t* sc = dp<uint8_t>(scratch);
@@ -320,6 +426,8 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
   const uint32_t nsp = 1u << (cdepth(L->dm) - 9), fs = L->sf ? L->fsd : 0;
   if (tier == LLB_MOE_EXACT && g_fused && T <= 8 && fg == fu && fused_supported(fg, fd, fs, nsp))
     return fused_forward(L, T, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt), sc, s);
+  if (tier == LLB_MOE_F16)
+    return gemm_forward(L, T, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt), sc, s);
   if ((rc = route(L, T, dp<float>(h2), dp<uint32_t>(ids), dp<float>(wt), sc, s))) return rc;
   const uint64_t rbg = row_bytes(fg, L->dm), rbu = row_bytes(fu, L->dm);
   const uint64_t esg = (uint64_t)(fz ? 2 : 1) * L->ef * rbg;

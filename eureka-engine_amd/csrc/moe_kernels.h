@@ -91,5 +91,24 @@ struct Q8Args {
   const float* x1;
   float* y;
 };
+struct GemmArgs {
+  const uint8_t* W0;  // weights (gate / the one matrix), rows of K columns
+  const uint8_t* W1;  // up (mode 0)
+  uint64_t es, rb;    // expert stride, row bytes
+  uint32_t K, N, M;   // M: rows when there is no tile list (the shared expert)
+  const _Float16* A;  // activations, f16 rows of K
+  const uint32_t* xmap;   // slot -> A row (mode 0), or null: slot itself
+  const uint32_t* off;    // [ne + 1] slot offsets
+  const uint32_t* tiles;  // tile list (e << 16 | tile), or null
+  const uint32_t* ntiles;
+  void* out;          // mode 0: f16 [slots][N]; mode 1: f32 [slots][N]
+};
+int launch_moe_gemm(const GemmArgs& g, uint32_t fm, uint32_t mode, uint32_t grid_y, hipStream_t st);
+size_t gemm_lds(uint32_t mode);
+uint32_t gemm_bm();
+int launch_to_f16(const float* x, _Float16* y, uint64_t n, hipStream_t st);
+int launch_tiles(const uint32_t* off, uint32_t ne, uint32_t* tiles, uint32_t* ntiles, hipStream_t st);
+int launch_combine(const float* out, const uint32_t* inv, const float* wt, uint32_t nk, const float* shd,
+                   const float* sgo, const float* x1, float* y, uint32_t dm, uint32_t T, hipStream_t st);
 int launch_dequant(uint32_t fm, const uint8_t* W, uint64_t rb, uint32_t rows, uint32_t cols, float* out,
                    hipStream_t st);

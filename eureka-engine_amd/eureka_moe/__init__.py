@@ -19,7 +19,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(HERE), "libeureka_moe.so")
 
 F32, Q8_0, Q4_K, Q6_K, Q5_K = 0, 1, 3, 4, 9
-EXACT, Q8 = 0, 1
+EXACT, Q8, F16 = 0, 1, 2
 BLOCK = {F32: (4, 1), Q8_0: (34, 32), Q4_K: (144, 256), Q6_K: (210, 256), Q5_K: (176, 256)}
 
 

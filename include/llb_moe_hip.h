@@ -40,6 +40,7 @@ typedef uint64_t llb_dptr; /* host/llb_backend.h:8-10 */
 /* numeric tiers */
 #define LLB_MOE_EXACT 0 /* the reference's exact tier: bit-identical to its f32 kernels */
 #define LLB_MOE_Q8 1    /* expert products on q8_1 activations (LLB_MOE_DP4A / LLB_PREFILL=fast) */
+#define LLB_MOE_F16 2   /* grouped expert GEMMs on MFMA, f16 operands, f32 accumulate (prefill) */
 
 /* ---- backend contract (host/llb_backend.h:8-41; CUDA twin host/llb_backend_cuda.h:186-219) ---- */
 int llb_hip_init(int device);                                  /* cuInit + context: gpu_load */

@@ -232,3 +232,36 @@ def test_dequant_every_f16_scale(dev):
     assert _nan_equal(got, ref)
     dev.free(p)
     dev.free(out)
+
+
+def _f16_case(dev, name, T, seed, sample=None):
+    shape = em.SHAPES[name]
+    _say("f16 tier", name, "T", T, "seed", seed)
+    layer = em.Layer(dev, shape, seed=seed)
+    run = em.Runner(dev, shape, T, tier=em.F16)
+    run.gen_inputs(seed)
+    run.forward(layer, residual=False)
+    y, ids, wt = run.outputs()
+    run.free()
+    layer.free()
+    h2, _ = ol.inputs(shape, seed, T)
+    toks = np.arange(T) if sample is None else np.random.default_rng(seed).choice(T, sample, replace=False)
+    hl = ol.HostLayer(shape, seed=seed, experts=[])
+    yr, idr, wtr, _ = hl.run(h2[toks], None)
+    assert np.array_equal(ids[toks], idr)  # routing is the exact tier's at every tier
+    assert np.array_equal(wt[toks].view(np.uint32), wtr.view(np.uint32))
+    m = ol.err_metrics(y[toks], yr)
+    _say("f16 tier vs exact oracle", m)
+    return m
+
+
+@pytest.mark.parametrize("name,T", [("c2", 8), ("c1", 64), ("c1k", 200)])
+def test_f16_tier_tolerance(dev, name, T):
+    m = _f16_case(dev, name, T, seed=21)
+    assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
+
+
+def test_f16_tier_prefill_2048_sampled(dev):
+    """config 4: 2048 tokens through the config-1 layer; 24 tokens checked against the oracle"""
+    m = _f16_case(dev, "c1", 2048, seed=0, sample=24)
+    assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
