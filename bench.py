@@ -38,6 +38,74 @@ def stage_bytes(shape, T=1):
     return {"route": route, "gate_up": gate_up, "down": down}
 
 
+MFMA_F16_PEAK_TFS = 2500.0
+
+
+def prefill(dev, shape, T, layers, steps, warmup):
+    """T-token chunks through `layers` resident layers on the f16 MFMA tier: tokens/s, and the gate/up
+    GEMM's MFMA rate (algorithmic flops 2 T nk dm ef x 2 per launch over its HIP-event time)."""
+    Ls = [em.Layer(dev, shape, seed=1, layer=100 + i) for i in range(layers)]
+    run = em.Runner(dev, shape, T, tier=em.F16)
+    run.gen_inputs(1)
+    dev.sync()
+    for _ in range(warmup):
+        for L in Ls:
+            run.forward(L)
+    dev.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        for L in Ls:
+            run.forward(L)
+    dev.sync()
+    wall = time.perf_counter() - t0
+    dev.timing(1)
+    dev.check(dev.lib.llb_hip_spin(20000))
+    for L in Ls:
+        run.forward(L)
+    st = dev.timing_read()
+    dev.timing(False)
+    gu_us = st["gate_up"][0]
+    flops = 2.0 * T * shape.nk * shape.dm * shape.ef * 2
+    ach = flops / (gu_us * 1e-6) / 1e12
+    wbytes = shape.ne * shape.ef * (em.row_bytes(shape.fg, shape.dm) + em.row_bytes(shape.fu, shape.dm))
+    run.free()
+    for L in Ls:
+        L.free()
+    us_layer = wall / (steps * layers) * 1e6
+    return {"tokens_per_s": round(T / (us_layer * 1e-6), 1), "us_per_layer_chunk": round(us_layer, 2), "T": T,
+            "layers": layers, "stages_us": {k: round(v[0], 2) for k, v in st.items()},
+            "roofline": {"bound": "mfma", "kernel": "gate_up GEMM (f16 MFMA)", "achieved": round(ach, 1),
+                         "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFS, 4),
+                         "weight_gbs": round(wbytes / (gu_us * 1e-6) / 1e9, 1)}}
+
+
+def batched(dev, shape, T, layers, steps, warmup, tier):
+    """config 3: T tokens a step through `layers` layers with the Zipf(1.1) router bias"""
+    Ls = [em.Layer(dev, shape, seed=3, layer=200 + i, bias=em.zipf_bias(shape.ne, 3 + i)) for i in range(layers)]
+    run = em.Runner(dev, shape, T, tier=tier)
+    run.gen_inputs(3)
+    for _ in range(warmup):
+        for L in Ls:
+            run.forward(L)
+    dev.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        for L in Ls:
+            run.forward(L)
+    dev.sync()
+    wall = time.perf_counter() - t0
+    ids = dev.read(run.ids, (T, shape.nk), np.uint32)
+    uniq = int(np.unique(ids).size)
+    run.free()
+    for L in Ls:
+        L.free()
+    us = wall / (steps * layers) * 1e6
+    byts = uniq * shape.expert_bytes() + shape.ne * shape.dm * 4 + shape.shared_bytes()
+    return {"us_per_layer": round(us, 2), "us_per_token_layer": round(us / T, 3), "T": T,
+            "unique_experts_last_layer": uniq, "algorithmic_bytes_last_layer": byts,
+            "hbm_frac_last_layer": round(byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def cpu_baseline(shape, seconds=12.0):
     """the CPU oracle's exact layer, single thread, on tokens of layer 0 (experts generated first)."""
     import oracle_lib as ol
@@ -71,6 +139,9 @@ def main():
     ap.add_argument("--tier", default="exact", choices=["exact", "q8"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", dest="graph", action="store_false", help="launch per layer instead of a graph")
+    ap.add_argument("--no-prefill", dest="prefill", action="store_false", help="skip the prefill leg")
+    ap.add_argument("--prefill-config", default="c1")
+    ap.add_argument("--prefill-T", type=int, default=2048)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the MoE path is not sharded across GPUs); "
@@ -151,6 +222,17 @@ def main():
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": sbytes[dom]},
     }
+    if args.prefill:
+        b3 = {}
+        for tn, tv in (("f16", em.F16), ("exact", em.EXACT)):
+            b3[tn] = batched(dev, em.SHAPES["c1"], 64, 4, max(2, args.steps // 4), 1, tv)
+        out["batched_c3"] = b3
+        for L in layers:
+            L.free()
+        layers.clear()
+        pshape = em.SHAPES[args.prefill_config]
+        out["prefill"] = prefill(dev, pshape, args.prefill_T, 4, max(2, args.steps // 4), 1)
+        out["prefill"]["config"] = f"{args.prefill_config} layer, {args.prefill_T}-token chunk, f16 MFMA tier"
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(shape)
     print(json.dumps(out), flush=True)

@@ -277,10 +277,12 @@ static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* 
   a.xstride = L->dm;
   a.tch = 16;
   const uint32_t ns = 1u << (cdepth(L->dm) - 9);
-  a.seg[0] = TreeSeg{dp<uint8_t>(L->router), LLB_FM_F32, (uint64_t)L->dm * 4, L->ne, lg, L->ne + 1};
-  a.seg[1] = TreeSeg{dp<uint8_t>(L->shgate), LLB_FM_F32, (uint64_t)L->dm * 4, L->sf ? 1u : 0u, lg + L->ne, L->ne + 1};
-  a.seg[2] = TreeSeg{dp<uint8_t>(L->SG), L->fsg, row_bytes(L->fsg, L->dm), L->sf, gsu, 2 * L->sf};
-  a.seg[3] = TreeSeg{dp<uint8_t>(L->SU), L->fsu, row_bytes(L->fsu, L->dm), L->sf, gsu + L->sf, 2 * L->sf};
+  a.seg[0] = TreeSeg{dp<uint8_t>(L->router), LLB_FM_F32, (uint64_t)L->dm * 4, L->ne, lg, L->ne + 1,
+                     dp<float>(L->router_bias)};
+  a.seg[1] = TreeSeg{dp<uint8_t>(L->shgate), LLB_FM_F32, (uint64_t)L->dm * 4, L->sf ? 1u : 0u, lg + L->ne, L->ne + 1,
+                     nullptr};
+  a.seg[2] = TreeSeg{dp<uint8_t>(L->SG), L->fsg, row_bytes(L->fsg, L->dm), L->sf, gsu, 2 * L->sf, nullptr};
+  a.seg[3] = TreeSeg{dp<uint8_t>(L->SU), L->fsu, row_bytes(L->fsu, L->dm), L->sf, gsu + L->sf, 2 * L->sf, nullptr};
   a.nseg = shared_rows ? 4 : 2;
   int rc;
   stage_begin(ST_ROUTE);
@@ -490,10 +492,12 @@ static int fused_forward(const llb_moe_layer* L, uint32_t T, const float* h2, co
   f.tr.T = T;
   f.tr.xstride = L->dm;
   f.tr.tch = 1;
-  f.tr.seg[0] = TreeSeg{dp<uint8_t>(L->router), LLB_FM_F32, (uint64_t)L->dm * 4, L->ne, lg, L->ne + 1};
-  f.tr.seg[1] = TreeSeg{dp<uint8_t>(L->shgate), LLB_FM_F32, (uint64_t)L->dm * 4, L->sf ? 1u : 0u, lg + L->ne, L->ne + 1};
-  f.tr.seg[2] = TreeSeg{dp<uint8_t>(L->SG), L->fsg, row_bytes(L->fsg, L->dm), L->sf, gsu, 2 * L->sf};
-  f.tr.seg[3] = TreeSeg{dp<uint8_t>(L->SU), L->fsu, row_bytes(L->fsu, L->dm), L->sf, gsu + L->sf, 2 * L->sf};
+  f.tr.seg[0] = TreeSeg{dp<uint8_t>(L->router), LLB_FM_F32, (uint64_t)L->dm * 4, L->ne, lg, L->ne + 1,
+                       dp<float>(L->router_bias)};
+  f.tr.seg[1] = TreeSeg{dp<uint8_t>(L->shgate), LLB_FM_F32, (uint64_t)L->dm * 4, L->sf ? 1u : 0u, lg + L->ne, L->ne + 1,
+                       nullptr};
+  f.tr.seg[2] = TreeSeg{dp<uint8_t>(L->SG), L->fsg, row_bytes(L->fsg, L->dm), L->sf, gsu, 2 * L->sf, nullptr};
+  f.tr.seg[3] = TreeSeg{dp<uint8_t>(L->SU), L->fsu, row_bytes(L->fsu, L->dm), L->sf, gsu + L->sf, 2 * L->sf, nullptr};
   f.tr.nseg = 4;
   const uint32_t rows = L->ne + (L->sf ? 1 + 2 * L->sf : 0);
   f.tk = TopkArgs{lg, L->ne + 1, L->ne, L->nk, L->sf ? 1u : 0u, L->sf, ids, wt, (float*)(sc + s.sgo)};

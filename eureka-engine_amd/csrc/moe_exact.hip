@@ -74,7 +74,7 @@ DEV void tree_body(const TreeArgs& a, u32 bx, u32 t, u32 L) {
     }
     float v = live ? tree_row_lane<NSP>(w, xv) : 0.0f;  // a dead lane's leaves are all +0 pads
     v = tree64_asc(v);
-    if (L == 0) sg.out[(u64)t * sg.ostride + row] = v;
+    if (L == 0) sg.out[(u64)t * sg.ostride + row] = sg.bias ? v + sg.bias[row] : v;
   }
 }
 template <u32 NSP>

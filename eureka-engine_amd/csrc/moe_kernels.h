@@ -14,6 +14,7 @@ struct TreeSeg {
   uint32_t rows;
   float* out;        // out[t * ostride + row]
   uint32_t ostride;
+  const float* bias; // added to row's dot (null: none)
 };
 struct TreeArgs {
   TreeSeg seg[4];

@@ -38,7 +38,7 @@ class MoeLayer(C.Structure):
     _fields_ = [("dm", C.c_uint32), ("ne", C.c_uint32), ("nk", C.c_uint32), ("ef", C.c_uint32), ("sf", C.c_uint32),
                 ("fx", C.c_uint32), ("fsg", C.c_uint32), ("fsu", C.c_uint32), ("fsd", C.c_uint32), ("pad", C.c_uint32),
                 ("router", C.c_uint64), ("shgate", C.c_uint64), ("G", C.c_uint64), ("U", C.c_uint64), ("D", C.c_uint64),
-                ("SG", C.c_uint64), ("SU", C.c_uint64), ("SD", C.c_uint64)]
+                ("SG", C.c_uint64), ("SU", C.c_uint64), ("SD", C.c_uint64), ("router_bias", C.c_uint64)]
 
 
 _SIGS = {
@@ -57,6 +57,12 @@ _SIGS = {
     "llb_hip_graph_end": (C.c_int, [C.POINTER(C.c_uint64)]),
     "llb_hip_graph_launch": (C.c_int, [C.c_uint64]),
     "llb_hip_graph_free": (C.c_int, [C.c_uint64]),
+    "llb_moe_table_check": (C.c_int, [C.POINTER(C.c_uint32), C.c_uint32, C.c_uint32, C.c_uint64]),
+    "llb_moe_layer_from_table": (C.c_int, [C.POINTER(C.c_uint32), C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64,
+                                           C.c_uint64, C.POINTER(MoeLayer)]),
+    "llb_moe_run_table": (C.c_int, [C.POINTER(C.c_uint32), C.c_uint32, C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64,
+                                    C.c_uint64, C.c_uint64, C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64,
+                                    C.c_uint64, C.c_uint64, C.c_size_t, C.c_int]),
     "llb_moe_hip_scratch_bytes": (C.c_size_t, [C.POINTER(MoeLayer), C.c_uint32, C.c_int]),
     "llb_moe_hip_forward": (C.c_int, [C.POINTER(MoeLayer), C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64,
                                       C.c_uint64, C.c_uint64, C.c_size_t, C.c_int]),
@@ -211,10 +217,18 @@ ST_ROUTER, ST_SHGATE, ST_G, ST_U, ST_D, ST_SG, ST_SU, ST_SD, ST_H2, ST_X1, ST_BI
 W_SIGMA = 0.02
 
 
+def zipf_bias(ne, seed, s=1.1):
+    """BASELINE config 3's skew: b_e = log z_e, z proportional to rank^-s over a seeded expert
+    permutation (ranks 1..ne), as f32"""
+    rank = np.empty(ne, np.int64)
+    rank[np.random.default_rng(seed).permutation(ne)] = np.arange(1, ne + 1)
+    return (-s * np.log(rank.astype(np.float64))).astype(np.float32)
+
+
 class Layer:
     """A synthetic MoE layer resident in HBM, generated on the device from (seed, layer)."""
 
-    def __init__(self, dev, shape, seed=0, layer=0):
+    def __init__(self, dev, shape, seed=0, layer=0, bias=None):
         self.dev, self.shape, self.seed, self.layer = dev, shape, seed, layer
         s, L = shape, layer * 16
         lib = dev.lib
@@ -237,11 +251,12 @@ class Layer:
             dev.check(lib.llb_moe_hip_gen_rows(s.fsg, seed, L + ST_SG, 0, s.sf, s.dm, W_SIGMA, self.SG))
             dev.check(lib.llb_moe_hip_gen_rows(s.fsu, seed, L + ST_SU, 0, s.sf, s.dm, W_SIGMA, self.SU))
             dev.check(lib.llb_moe_hip_gen_rows(s.fsd, seed, L + ST_SD, 0, s.dm, s.sf, W_SIGMA, self.SD))
+        self.bias = dev.upload(np.asarray(bias, np.float32)) if bias is not None else 0
         self.desc = MoeLayer(s.dm, s.ne, s.nk, s.ef, s.sf, s.fx, s.fsg, s.fsu, s.fsd, 0, self.router, self.shgate,
-                             self.G, self.U, self.D, self.SG, self.SU, self.SD)
+                             self.G, self.U, self.D, self.SG, self.SU, self.SD, self.bias)
 
     def free(self):
-        for p in (self.router, self.shgate, self.G, self.U, self.D, self.SG, self.SU, self.SD):
+        for p in (self.router, self.shgate, self.G, self.U, self.D, self.SG, self.SU, self.SD, self.bias):
             if p:
                 self.dev.free(p)
 

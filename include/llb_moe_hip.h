@@ -79,7 +79,22 @@ typedef struct {
   llb_dptr shgate; /* F32 [dm] (word 22); 0 when sf == 0 */
   llb_dptr G, U, D;    /* expert stacks; U ignored when fused (U = G + ef rows, llb_host.c:677) */
   llb_dptr SG, SU, SD; /* shared expert */
+  llb_dptr router_bias; /* F32 [ne] added to each router logit, one rounding (0: none). Not in the
+                         * reference: BASELINE config 3 skews expert load with it */
 } llb_moe_layer;
+
+/* ---- the layer's table row (host code) ----
+ * w: the layer's 32 raw table.bin words (tools/gguf2pack.c:1142-1146): w[21] router, w[22] shared
+ * gate row, w[3..5] shared gate / up / down (offset | fm << 28), w[26] formats, w[27] ne, w[28] ef,
+ * w[29] sf, w[30] nk. check: pass_mail's MoE admission (tools/payload-moeany.patch:26-50), 0 or 8.
+ * from_table: llb_moe_run's field decode (host/llb_host.c:623-627), base = the layer's Bytes.
+ * run_table: both, then llb_moe_hip_forward (the call site's one-line replacement). */
+int llb_moe_table_check(const uint32_t* w, uint32_t dm, uint32_t df, uint64_t len);
+int llb_moe_layer_from_table(const uint32_t* w, uint32_t dm, llb_dptr base, llb_dptr G, llb_dptr U, llb_dptr D,
+                             llb_moe_layer* out);
+int llb_moe_run_table(const uint32_t* w, uint32_t dm, uint32_t df, uint64_t len, llb_dptr base, llb_dptr G,
+                      llb_dptr U, llb_dptr D, uint32_t T, llb_dptr h2, llb_dptr x1, llb_dptr y, llb_dptr ids,
+                      llb_dptr wt, llb_dptr scratch, size_t scratch_bytes, int tier);
 
 /* bytes of scratch llb_moe_hip_forward needs for T tokens at a tier (llb_scratch, host/llb_host.c:634) */
 size_t llb_moe_hip_scratch_bytes(const llb_moe_layer* L, uint32_t T, int tier);

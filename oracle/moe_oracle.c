@@ -356,8 +356,10 @@ float mo_silu_mul(float g, float u) { return (g / (1.0f + mo_exp(-g))) * u; }
 /* ------------------------------------------------------------------ routing */
 
 void mo_router(const mo_layer* L, const float* h2, float* lg, float* sg) {
-  for (u32 e = 0; e < L->ne; e++)
+  for (u32 e = 0; e < L->ne; e++) {
     lg[e] = mo_gemv_row(MO_F32, (const u8*)(L->router + (size_t)e * L->dm), L->dm, h2);
+    if (L->router_bias) lg[e] = lg[e] + L->router_bias[e];
+  }
   *sg = L->shgate ? mo_gemv_row(MO_F32, (const u8*)L->shgate, L->dm, h2) : 0.0f;
 }
 
@@ -658,6 +660,7 @@ int mo_moe_f64(const mo_layer* L, u32 T, const float* h2, const u32* ids, double
     for (u32 e = 0; e < ne; e++) {
       double a = 0.0;
       for (u32 c = 0; c < dm; c++) a += (double)L->router[(size_t)e * dm + c] * (double)h[c];
+      if (L->router_bias) a += (double)L->router_bias[e];
       lg[e] = a;
       mx = a > mx ? a : mx;
     }

@@ -28,7 +28,8 @@ class MoLayer(C.Structure):
                 ("fg", C.c_uint32), ("fu", C.c_uint32), ("fd", C.c_uint32),
                 ("fsg", C.c_uint32), ("fsu", C.c_uint32), ("fsd", C.c_uint32),
                 ("router", C.c_void_p), ("shgate", C.c_void_p), ("G", C.c_void_p), ("U", C.c_void_p),
-                ("D", C.c_void_p), ("SG", C.c_void_p), ("SU", C.c_void_p), ("SD", C.c_void_p)]
+                ("D", C.c_void_p), ("SG", C.c_void_p), ("SU", C.c_void_p), ("SD", C.c_void_p),
+                ("router_bias", C.c_void_p)]
 
 
 P = C.c_void_p
@@ -112,7 +113,8 @@ def deq(fm, row, cols):
 class HostLayer:
     """Host copy of a synthetic layer. experts=None: every expert; else only those (others zero)."""
 
-    def __init__(self, shape, seed=0, layer=0, experts=None):
+    def __init__(self, shape, seed=0, layer=0, experts=None, bias=None):
+        self.bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
         s, L = shape, layer * 16
         self.shape = s
         self.router = gen_rows(F32, seed, L + ST_ROUTER, 0, s.ne, s.dm).view(np.float32)
@@ -144,7 +146,7 @@ class HostLayer:
         s = self.shape
         self.desc = MoLayer(s.dm, s.ne, s.nk, s.ef, s.sf, s.fg, s.fu, s.fd, s.fsg, s.fsu, s.fsd,
                             ptr(self.router), ptr(self.shgate), ptr(self.G), ptr(self.U), ptr(self.D),
-                            ptr(self.SG), ptr(self.SU), ptr(self.SD))
+                            ptr(self.SG), ptr(self.SU), ptr(self.SD), ptr(self.bias))
 
     def route(self, h2):
         """ids, wt, sgo per token, the exact tier's routing."""

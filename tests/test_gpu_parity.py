@@ -265,3 +265,33 @@ def test_f16_tier_prefill_2048_sampled(dev):
     """config 4: 2048 tokens through the config-1 layer; 24 tokens checked against the oracle"""
     m = _f16_case(dev, "c1", 2048, seed=0, sample=24)
     assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
+
+
+@pytest.mark.parametrize("tier", [em.EXACT, em.F16, em.Q8])
+def test_batched_zipf_config3(dev, tier):
+    """config 3: 64 tokens through the config-1 layer with a Zipf(1.1) router bias (skewed loads)"""
+    shape, T, seed = em.SHAPES["c1"], 64, 3
+    bias = em.zipf_bias(shape.ne, seed)
+    _say("config 3, tier", tier)
+    layer = em.Layer(dev, shape, seed=seed, bias=bias)
+    run = em.Runner(dev, shape, T, tier=tier)
+    run.gen_inputs(seed)
+    run.forward(layer)
+    y, ids, wt = run.outputs()
+    run.free()
+    layer.free()
+    h2, x1 = ol.inputs(shape, seed, T)
+    hl = ol.HostLayer(shape, seed=seed, experts=[], bias=bias)
+    counts = np.bincount(ids.ravel(), minlength=shape.ne)
+    _say("experts hit", int((counts > 0).sum()), "max load", int(counts.max()))
+    assert counts.max() >= 20 and (counts == 0).sum() > shape.ne // 4  # the skew the config asks for
+    if tier == em.EXACT:
+        yr, idr, wtr, _ = hl.run(h2, x1)
+        assert np.array_equal(ids, idr) and np.array_equal(wt.view(np.uint32), wtr.view(np.uint32))
+        assert np.array_equal(y.view(np.uint32), yr.view(np.uint32))
+    else:
+        yr, idr, _, _ = hl.run(h2, x1, tier="exact" if tier == em.F16 else "q8")
+        assert np.array_equal(ids, idr)
+        m = ol.err_metrics(y - x1, yr - x1)
+        _say("vs oracle", m)
+        assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999
