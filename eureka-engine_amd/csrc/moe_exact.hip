@@ -18,6 +18,16 @@
 #include "moe_dev.h"
 #include "moe_kernels.h"
 
+// phase timestamps for latency studies: a build that defines MOE_PHASE_T gets (block 0, thread 0)
+// wall-clock stamps (100 MHz) in moe_phase_t[]; the library build compiles them away
+#ifdef MOE_PHASE_T
+__device__ unsigned long long moe_phase_t[64];
+#define PHASE(i) \
+  do { if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) moe_phase_t[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define PHASE(i) do {} while (0)
+#endif
+
 // ---------------------------------------------------------------- tree rows (router, shared)
 
 template <u32 NSP>
@@ -53,6 +63,7 @@ DEV void span_any(u32 fm, const u8* rp, u32 c0, float* w) {
 // leaves [L S, L S + S); blockDim 64, grid (ceil(rows / TREE_RPW), T)
 template <u32 NSP>
 DEV void tree_body(const TreeArgs& a, u32 bx, u32 t, u32 L) {
+  PHASE(24);
   const u32 c0 = 32 * NSP * L;
   const bool live = c0 < a.cols;  // pad leaves past cols count +0
   float4 xv[8 * NSP];
@@ -72,9 +83,11 @@ DEV void tree_body(const TreeArgs& a, u32 bx, u32 t, u32 L) {
 #pragma unroll
         for (u32 i = 0; i < 32; i++) w[32 * q + i] = 0.0f;
     }
+    PHASE(25 + 2 * k);
     float v = live ? tree_row_lane<NSP>(w, xv) : 0.0f;  // a dead lane's leaves are all +0 pads
     v = tree64_asc(v);
     if (L == 0) sg.out[(u64)t * sg.ostride + row] = sg.bias ? v + sg.bias[row] : v;
+    PHASE(26 + 2 * k);
   }
 }
 template <u32 NSP>
@@ -95,76 +108,162 @@ DEV void wave_amax(float& bv, u32& bi) {
   amax_step(bv, bi, dppf<DPP_XOR2>(bv), dppu<DPP_XOR2>(bi));
   amax_step(bv, bi, dppf<DPP_UP4>(bv), dppu<DPP_UP4>(bi));
   amax_step(bv, bi, dppf<DPP_XOR8>(bv), dppu<DPP_XOR8>(bi));
-  // lanes 0 mod 16 now hold their row's best; take rows 0..3's through readlane
-  float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), 0));
-  u32 i0 = (u32)__builtin_amdgcn_readlane((int)bi, 0);
-#pragma unroll
-  for (int r = 16; r < 64; r += 16)
-    amax_step(v0, i0, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), r)),
-              (u32)__builtin_amdgcn_readlane((int)bi, r));
-  bv = v0;
-  bi = i0;
+  // every lane holds its row's best: the other row of the pair, then the other half
+  {
+    const auto v = __builtin_amdgcn_permlane16_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
+    const auto i = __builtin_amdgcn_permlane16_swap(bi, bi, false, false);
+    float v0 = __uint_as_float(v[0]);
+    u32 i0 = i[0];
+    amax_step(v0, i0, __uint_as_float(v[1]), i[1]);
+    bv = v0;
+    bi = i0;
+  }
+  {
+    const auto v = __builtin_amdgcn_permlane32_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
+    const auto i = __builtin_amdgcn_permlane32_swap(bi, bi, false, false);
+    float v0 = __uint_as_float(v[0]);
+    u32 i0 = i[0];
+    amax_step(v0, i0, __uint_as_float(v[1]), i[1]);
+    bv = v0;
+    bi = i0;
+  }
 }
 
-// one wave a token (ne <= 1024), llb_moe_topk's arithmetic: mx = max; v = exp(l - mx); the sum in
-// the 1024-thread block's order (thread t = expert t: each 32-expert group by the xor tree 16 .. 1,
-// then the group sums in order); p = v (1 / sum); the k largest p, ties to the lower index;
-// wt_j = p / max(sum of the k p in rank order, 2^-14); sgo = sigmoid(sg)
-DEV void topk_body(const TopkArgs& a, u32 t, u32 L) {
+// one block of 256 a token (ne <= 1024), llb_moe_topk's arithmetic: mx = max; v = exp(l - mx); the
+// sum in the 1024-thread block's order (expert e on thread e: each 32-expert group by the xor tree
+// 16 .. 1, then the group sums in order); p = v (1 / sum). Selection by rank instead of k argmax
+// rounds: rank(e) = #{e' : p_e' > p_e, or p_e' = p_e and e' < e} is the round in which repeated
+// argmax (ties to the lower index) would take e, so the experts with rank < k are the top k in that
+// order -- independent compares, no serial chain. wt_j = p / max(sum of the k p in rank order,
+// 2^-14); sgo = sigmoid(sg). Thread t holds experts t, t + 256, t + 512, t + 768.
+DEV void topk_body256(const TopkArgs& a, u32 t, float* sm) {
+  float* ps = sm;               // [ne] p
+  float* red = sm + 1024;       // [32] group sums / wave maxima, [32] tau, [40] count, [64..128) lane maxima
+  float* wv = sm + 1152;        // [64] the chosen p by rank, then [256] + [256] candidates
+  const u32 tid = threadIdx.x, L = tid & 63, w = tid >> 6;
+  PHASE(0);
   const float* lg = a.lg + (u64)t * a.lstride;
-  const u32 ni = (a.ne + 63) / 64;
-  float p[16];
+  const u32 ni = (a.ne + 255) / 256;
+  float p[4];
   float mx = bits_f(0xFF800000u);
 #pragma unroll
-  for (u32 i = 0; i < 16; i++) {
-    const u32 e = L + 64 * i;
-    const bool ok = i < ni && e < a.ne;
-    p[i] = ok ? lg[e] : 0.0f;
-    if (ok) mx = fmaxf(mx, p[i]);
+  for (u32 i = 0; i < 4; i++) {
+    const u32 e = tid + 256 * i;
+    p[i] = (i < ni && e < a.ne) ? lg[e] : 0.0f;
+    if (i < ni && e < a.ne) mx = fmaxf(mx, p[i]);
   }
+  PHASE(1);
   {
     u32 dummy = 0;
     wave_amax(mx, dummy);
   }
-  float tot = 0.0f;
+  if (L == 0) red[w] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  PHASE(2);
 #pragma unroll
-  for (u32 i = 0; i < 16; i++) {
+  for (u32 i = 0; i < 4; i++) {
     if (i < ni) {
-      const u32 e = L + 64 * i;
+      const u32 e = tid + 256 * i;
       p[i] = e < a.ne ? exp_f(p[i] - mx) : 0.0f;
       const float s = tree32_desc(p[i]);
-      tot = tot + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
-      if (64 * i + 32 < a.ne) tot = tot + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 32));
+      if ((L & 31) == 0) red[(tid >> 5) + 8 * i] = s;  // group (e / 32)
     }
   }
+  __syncthreads();
+  float tot = 0.0f;
+  const u32 ng = (a.ne + 31) / 32;
+  for (u32 g = 0; g < ng; g++) tot = tot + red[g];
   const float inv = 1.0f / tot;
 #pragma unroll
-  for (u32 i = 0; i < 16; i++) p[i] = (i < ni && L + 64 * i < a.ne) ? p[i] * inv : -1.0f;
+  for (u32 i = 0; i < 4; i++) {
+    const u32 e = tid + 256 * i;
+    if (i < ni && e < a.ne) { p[i] = p[i] * inv; ps[e] = p[i]; }
+  }
+  __syncthreads();
+  PHASE(3);
+  // prune: tau = the k-th largest of the 64 strided maxima m_l = max p[l + 64 j]; at least k values
+  // are >= tau, so the k-th largest value is >= tau and every expert of the top k has p >= tau
+  u32* cnt = (u32*)(red + 40);
+  float* cv = wv + 64;                 // [256] candidate p
+  u32* ci = (u32*)(cv + 256);          // [256] candidate expert
+  float* lm = red + 64;                // [64] lane maxima (past red's 32 + the counters)
+  if (tid < 64) {
+    float m = ps[tid];
+    for (u32 e = tid + 64; e < a.ne; e += 64) m = fmaxf(m, ps[e]);
+    lm[tid] = tid < a.ne ? m : bits_f(0xFF800000u);
+  }
+  if (tid == 64) *cnt = 0;
+  __syncthreads();
+  {
+    const float m = lm[tid & 63];
+    u32 r = 0;
+#pragma unroll
+    for (u32 q = 16 * w; q < 16 * w + 16; q++) r += (lm[q] > m || (lm[q] == m && q < (tid & 63)));
+    ((u32*)cv)[tid] = r;               // partial ranks, reused below
+  }
+  __syncthreads();
+  if (tid < 64) {
+    const u32* pr = (const u32*)cv;
+    const u32 r = pr[tid] + pr[tid + 64] + pr[tid + 128] + pr[tid + 192];
+    if (r == a.nk - 1) red[32] = lm[tid];
+  }
+  __syncthreads();
+  const float tau = red[32];
+#pragma unroll
+  for (u32 i = 0; i < 4; i++) {
+    const u32 e = tid + 256 * i;
+    if (i < ni && e < a.ne && p[i] >= tau) {
+      const u32 s = atomicAdd(cnt, 1u);
+      if (s < 256) { cv[s] = p[i]; ci[s] = e; }
+    }
+  }
+  __syncthreads();
+  const u32 nc = *cnt;
   u32* ids = a.ids + (u64)t * a.nk;
-  float* wt = a.wt + (u64)t * a.nk;
-  float s = 0.0f, mine = 0.0f;
-  for (u32 j = 0; j < a.nk; j++) {
-    float bv = -1.0f;
-    u32 bi = 0xffffffffu;
+  if (nc <= 256) {
+    // rank among the candidates (all of the top k are among them, so ranks below k agree)
+    if (tid < nc) {
+      const float v = cv[tid];
+      const u32 me = ci[tid];
+      u32 r = 0;
+      for (u32 q = 0; q < nc; q++) r += (cv[q] > v || (cv[q] == v && ci[q] < me));
+      if (r < a.nk) { ids[r] = me; wv[r] = v; }
+    }
+  } else {
+    // heavy ties: rank over every expert
+    u32 rk[4] = {0, 0, 0, 0};
+    for (u32 q = 0; q < a.ne; q++) {
+      const float v = ps[q];
 #pragma unroll
-    for (u32 i = 0; i < 16; i++)
-      if (p[i] > bv) { bv = p[i]; bi = L + 64 * i; }
-    wave_amax(bv, bi);
+      for (u32 i = 0; i < 4; i++) rk[i] += (v > p[i] || (v == p[i] && q < tid + 256 * i));
+    }
 #pragma unroll
-    for (u32 i = 0; i < 16; i++)
-      if (L + 64 * i == bi) p[i] = -2.0f;
-    s = s + bv;          // the rank-order sum, uniform across the wave
-    if (L == j) mine = bv;
-    if (L == 0) ids[j] = bi;
+    for (u32 i = 0; i < 4; i++) {
+      const u32 e = tid + 256 * i;
+      if (i < ni && e < a.ne && rk[i] < a.nk) { ids[rk[i]] = e; wv[rk[i]] = p[i]; }
+    }
   }
-  s = s < 6.103515625e-5f ? 6.103515625e-5f : s;
-  if (L < a.nk) wt[L] = mine / s;
-  if (L == 0) {
-    const float sg = a.has_sg ? lg[a.ne] : 0.0f;
-    a.sgo[t] = 1.0f / (1.0f + exp_f(-sg));
+  __syncthreads();
+  PHASE(4);
+  if (tid < 64) {
+    float s = 0.0f;
+    for (u32 j = 0; j < a.nk; j++) s = s + wv[j];
+    s = s < 6.103515625e-5f ? 6.103515625e-5f : s;
+    if (tid < a.nk) a.wt[(u64)t * a.nk + tid] = wv[tid] / s;
+    if (tid == 0) {
+      const float sg = a.has_sg ? lg[a.ne] : 0.0f;
+      a.sgo[t] = 1.0f / (1.0f + exp_f(-sg));
+    }
   }
+  PHASE(5);
 }
-__global__ void __launch_bounds__(64) k_topk(TopkArgs a) { topk_body(a, blockIdx.x, threadIdx.x); }
+
+__global__ void __launch_bounds__(256) k_topk(TopkArgs a) {
+  __shared__ float sm[1024 + 128 + 64 + 512];
+  topk_body256(a, blockIdx.x, sm);
+}
 
 // ---------------------------------------------------------------- stride rows (experts)
 //
@@ -210,6 +309,7 @@ template <u32 FG, u32 FU>
 DEV void gu_body(const GuArgs& a, u32 np, u32 bx, float* sm) {
   float* xs = sm;              // [dm]
   float* lv = sm + a.dm;       // [2 np][dm / 4]
+  PHASE(8);
   const u32 task0 = bx * np, slot = task0 / a.ef, r0 = task0 % a.ef;
   const u32 t = slot / a.nk;
   const float* x = a.h2 + (u64)t * a.dm;
@@ -217,6 +317,7 @@ DEV void gu_body(const GuArgs& a, u32 np, u32 bx, float* sm) {
   const u64 e = a.ids[slot];
   const u32 ns = a.dm / 32, ng = a.dm / 4, nr = 2 * np;
   __syncthreads();
+  PHASE(9);
   const bool walk = 256 % ns == 0;  // fixed span column a thread: x read once for its rows
   for (u32 it = threadIdx.x; it < (walk ? ns * (256 / ns) : nr * ns); it += 256) {
     const u32 c = it % ns;
@@ -233,7 +334,9 @@ DEV void gu_body(const GuArgs& a, u32 np, u32 bx, float* sm) {
       store_leaves(lv + rr * ng + 8 * c, l);
     }
   }
+  PHASE(10);
   __syncthreads();
+  PHASE(11);
   const u32 rr = threadIdx.x >> 5, v = threadIdx.x & 31;
   for (u32 rb = 0; rb < nr; rb += 8) {
     const u32 r = rb + rr;
@@ -242,6 +345,7 @@ DEV void gu_body(const GuArgs& a, u32 np, u32 bx, float* sm) {
     const float u = xpeer32(s);  // the up row sits in the other half of the wave
     if (r < nr && (r & 1) == 0 && v == 0) a.act[(u64)slot * a.ef + r0 + (r >> 1)] = silu_mul(s, u);
   }
+  PHASE(12);
 }
 template <u32 FG, u32 FU>
 __global__ void __launch_bounds__(256) k_gu_exact(GuArgs a, u32 np) {
@@ -259,11 +363,13 @@ DEV void dn_body(const DnArgs& a, u32 bx, u32 t, float* sm) {
   float* lv = sm;                                  // [rw][nk ef / 4 + sf / 4]
   float* sa = sm + a.rw * per_row;                 // [sf]
   float* part = sa + (FS ? a.sf : 0u);             // [rw][nt]
+  PHASE(16);
   if (FS) {
     const float* g = a.gsu + (u64)t * 2 * a.sf;
     for (u32 i = threadIdx.x; i < a.sf; i += 256) sa[i] = silu_mul(g[i], g[a.sf + i]);
     __syncthreads();
   }
+  PHASE(17);
   const float* act = a.act + (u64)t * a.nk * a.ef;
   // column q = one 32-column span of one task: q < nk ef / 32 routed (task q / (ef / 32)), then
   // the shared expert's; a thread loads its x slice once and walks the block's rw rows
@@ -286,7 +392,9 @@ DEV void dn_body(const DnArgs& a, u32 bx, u32 t, float* sm) {
       store_leaves(lv + rl * per_row + j * nge + 8 * sp, l);
     }
   }
+  PHASE(18);
   __syncthreads();
+  PHASE(19);
   const u32 sums = a.rw * nt * 32;
   for (u32 q = threadIdx.x; q < ((sums + 63) & ~63u); q += 256) {
     const u32 k = q >> 5, v = q & 31;  // k = rl nt + j
@@ -311,6 +419,7 @@ DEV void dn_body(const DnArgs& a, u32 bx, u32 t, float* sm) {
       a.y[(u64)t * a.dm + r] = FS ? (mo + pr[a.nk] * a.sgo[t]) + res : mo + res;
     }
   }
+  PHASE(20);
 }
 template <u32 FD, u32 FS>
 __global__ void __launch_bounds__(256) k_dn_exact(DnArgs a) {
@@ -382,7 +491,7 @@ __global__ void __launch_bounds__(256) k_fused(FusedArgs f) {
       item_done(&c[1]);
     } else if (it < e2) {
       phase_wait(&c[1], f.nR, &c[5], f.spin);
-      if (w == 0) topk_body(f.tk, it - e1, L);
+      topk_body256(f.tk, it - e1, sm);
       item_done(&c[2]);
     } else if (it < e3) {
       phase_wait(&c[2], nK, &c[5], f.spin);
@@ -431,7 +540,7 @@ int launch_tree_rows(const TreeArgs& a, u32 nsp, hipStream_t st) {
 }
 
 int launch_topk(const TopkArgs& a, u32 T, hipStream_t st) {
-  hipLaunchKernelGGL(k_topk, dim3(T), dim3(64), 0, st, a);
+  hipLaunchKernelGGL(k_topk, dim3(T), dim3(256), 0, st, a);
   return 0;
 }
 
@@ -475,7 +584,9 @@ size_t fused_lds(const FusedArgs& f) {
   const size_t gu = ((size_t)f.gu.dm + (size_t)2 * f.np * (f.gu.dm / 4)) * 4;
   const u32 nt = f.dn.nk + (f.dn.sf ? 1u : 0u);
   const size_t dn = ((size_t)f.dn.rw * (f.dn.nk * f.dn.ef / 4 + f.dn.sf / 4) + f.dn.sf + f.dn.rw * nt) * 4;
-  return gu > dn ? gu : dn;
+  const size_t tk = (size_t)(1024 + 128 + 64 + 512) * 4;  // topk_body256's LDS
+  const size_t m = gu > dn ? gu : dn;
+  return m > tk ? m : tk;
 }
 
 int launch_fused(const FusedArgs& f, u32 fg, u32 fd, u32 fs, u32 nsp, u32 grid, hipStream_t st) {
