@@ -266,8 +266,10 @@ size_t llb_moe_hip_scratch_bytes(const llb_moe_layer* L, uint32_t T, int tier) {
 }
 
 // router + shared gate logit + shared gate / up (the tree rows), then top-k and sa
+// the router / shared rows launch, then top-k -- or, with defer, top-k's arguments for a later
+// launch that routes in-kernel
 static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* ids, float* wt, uint8_t* sc,
-                 const ExactScratch& s, bool shared_rows = true) {
+                 const ExactScratch& s, bool shared_rows = true, TopkArgs* defer = nullptr) {
   float* lg = (float*)(sc + s.lg);
   float* gsu = (float*)(sc + s.gsu);
   TreeArgs a{};
@@ -298,6 +300,10 @@ static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* 
   k.ids = ids;
   k.wt = wt;
   k.sgo = (float*)(sc + s.sgo);
+  if (defer) {
+    *defer = k;
+    return 0;
+  }
   stage_begin(ST_TOPK);
   rc = launched(launch_topk(k, T, g_stream), "topk");
   stage_end(ST_TOPK);
@@ -430,7 +436,11 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
     return fused_forward(L, T, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt), sc, s);
   if (tier == LLB_MOE_F16)
     return gemm_forward(L, T, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt), sc, s);
-  if ((rc = route(L, T, dp<float>(h2), dp<uint32_t>(ids), dp<float>(wt), sc, s))) return rc;
+  // the exact tier routes inside its gate / up launch (one launch fewer a layer)
+  TopkArgs tk{};
+  const bool fuse_topk = tier == LLB_MOE_EXACT && fg == fu;
+  if ((rc = route(L, T, dp<float>(h2), dp<uint32_t>(ids), dp<float>(wt), sc, s, true, fuse_topk ? &tk : nullptr)))
+    return rc;
   const uint64_t rbg = row_bytes(fg, L->dm), rbu = row_bytes(fu, L->dm);
   const uint64_t esg = (uint64_t)(fz ? 2 : 1) * L->ef * rbg;
   const uint8_t* G = dp<uint8_t>(L->G);
@@ -454,7 +464,8 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
   g.act = (float*)(sc + s.act);
   g.es = esg;
   stage_begin(ST_GU);
-  if ((rc = launched(launch_gu_exact(g, fg, fu, T * L->nk, g_stream), "expert gate/up"))) return rc;
+  rc = fuse_topk ? launch_gu_topk(g, tk, fg, fu, T * L->nk, g_stream) : launch_gu_exact(g, fg, fu, T * L->nk, g_stream);
+  if ((rc = launched(rc, fuse_topk ? "top-k + expert gate/up" : "expert gate/up"))) return rc;
   stage_end(ST_GU);
   DnArgs d{};
   d.D = dp<uint8_t>(L->D);

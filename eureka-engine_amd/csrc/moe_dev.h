@@ -26,6 +26,7 @@ typedef uint8_t u8;
 #define FM_Q5_K 9u
 
 #define DEV static __device__ __forceinline__
+#define MDEV __device__ __forceinline__  // member functions
 
 DEV float bits_f(u32 u) { return __uint_as_float(u); }
 
@@ -39,15 +40,25 @@ DEV float f16v(u32 h) {
   return bits_f(((h & 0x7c00u) == 0x7c00u && (h & 1023u)) ? nan : __float_as_uint(hw));
 }
 
+// a word the compiler may not look through: keeps "mask 4 bytes, then v_cvt_f32_ubyte{0..3}" from
+// being rewritten into one bit-field extract per byte
+DEV u32 opq(u32 v) {
+  __asm__("" : "+v"(v));
+  return v;
+}
 // byte k of v as an exact float (v_cvt_f32_ubyte{0..3})
 DEV float ubyte(u32 v, u32 k) { return (float)((v >> (8 * k)) & 255u); }
 
 DEV u32 ld_u16(const u8* p) { return (u32)*(const unsigned short*)p; }
 
+// p rounded down to 4 bytes by pointer arithmetic (a cast through an integer would hide the global
+// address space and turn every load through it into a flat load, which also holds up LDS waits)
+DEV const u32* al4(const u8* p) { return (const u32*)(p - ((u32)(uintptr_t)p & 3u)); }
+
 // 32 bytes from a 2-aligned address: nine aligned dwords, funnel-shifted by 16 when p % 4 == 2.
 // Reads at most 4 bytes past p + 32 (every caller's span has them inside its own block).
 DEV void ld32_a2(const u8* p, u32 o[8]) {
-  const u32* a = (const u32*)((uintptr_t)p & ~(uintptr_t)3);
+  const u32* a = al4(p);
   const u32 sh = ((u32)(uintptr_t)p & 2u) * 8u;
   u32 w[9];
 #pragma unroll
@@ -90,7 +101,7 @@ template <> struct Span<FM_F32> {
 template <> struct Span<FM_Q8_0> {
   DEV void w(const u8* row, u32 c0, float* w) {
     const u8* B = row + (u64)(c0 >> 5) * 34u;
-    const u32* a = (const u32*)((uintptr_t)B & ~(uintptr_t)3);
+    const u32* a = al4(B);
     const bool odd = ((uintptr_t)B & 2u) != 0;
     u32 v[9];
 #pragma unroll
@@ -174,6 +185,149 @@ template <> struct Span<FM_Q6_K> {
 #pragma unroll
       for (int t = 0; t < 4; t++)
         w[4 * k + t] = (k < 4 ? ds0 : ds1) * (ubyte(v, t) - 32.0f);
+    }
+  }
+};
+
+// ---- half spans: columns c0 + 16 jh .. c0 + 16 jh + 15 of the span at c0, in two steps -- ld
+// issues the raw loads (so a caller can put a row's loads in flight before it waits on anything
+// else), dec turns them into the same 16 weights span_w gives for those columns.
+
+// 16 bytes from a 2-aligned address, never reading outside p .. p + 15: four aligned dwords from
+// p rounded down, and, when p % 4 == 2, the half dword at p + 14 that the funnel shift by 16 needs.
+// When p % 4 == 0 that fifth word is unused and is read from p + 12 instead (p + 16 can be past the
+// end of the buffer: a Q8_0 block's second half ends 2 bytes before a 4-aligned boundary).
+struct Raw16 { u32 w[5]; };
+DEV Raw16 ld16_a2(const u8* p) {
+  const u32 odd = (u32)(uintptr_t)p & 2u;
+  const u32* a = al4(p);
+  Raw16 r;
+#pragma unroll
+  for (int k = 0; k < 4; k++) r.w[k] = a[k];
+  r.w[4] = (u32)*(const unsigned short*)((const u8*)a + (odd ? 16 : 12));
+  return r;
+}
+DEV void al16(const Raw16& r, u32 sh, u32 o[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; k++) o[k] = __builtin_amdgcn_alignbit(r.w[k + 1], r.w[k], sh);
+}
+
+template <u32 F> struct Half;
+
+template <> struct Half<FM_F32> {
+  float4 v[4];
+  MDEV void ld(const u8* row, u32 c0, u32 jh) {
+    const float4* p = (const float4*)(row + 4 * (u64)(c0 + 16 * jh));
+#pragma unroll
+    for (int k = 0; k < 4; k++) v[k] = p[k];
+  }
+  MDEV void dec(u32, u32, float* w) const {
+#pragma unroll
+    for (int k = 0; k < 4; k++) { w[4 * k] = v[k].x; w[4 * k + 1] = v[k].y; w[4 * k + 2] = v[k].z; w[4 * k + 3] = v[k].w; }
+  }
+};
+
+template <> struct Half<FM_Q8_0> {
+  Raw16 q;
+  u32 d, sh;
+  MDEV void ld(const u8* row, u32 c0, u32 jh) {
+    const u8* B = row + (u64)(c0 >> 5) * 34u;
+    d = ld_u16(B);
+    const u8* p = B + 2 + 16 * jh;
+    sh = ((u32)(uintptr_t)p & 2u) * 8u;
+    q = ld16_a2(p);
+  }
+  MDEV void dec(u32, u32, float* w) const {
+    const float dv = f16v(d);
+    u32 o[4];
+    al16(q, sh, o);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const u32 v = opq(o[k] ^ 0x80808080u);
+#pragma unroll
+      for (int t = 0; t < 4; t++) w[4 * k + t] = (ubyte(v, t) - 128.0f) * dv;
+    }
+  }
+};
+
+template <> struct Half<FM_Q4_K> {
+  uint4 h, q;
+  MDEV void ld(const u8* row, u32 c0, u32 jh) {
+    const u8* B = row + (u64)(c0 >> 8) * 144u;
+    const u32 j = (c0 & 255u) >> 5;
+    h = *(const uint4*)B;
+    q = *(const uint4*)(B + 16 + 32 * (j >> 1) + 16 * jh);
+  }
+  // an odd sub-block's codes are the high nibbles: masked in place they read 16 q, and d sc / 16
+  // (exact: a power-of-two scale of a normal float) times 16 q is the same exact product
+  MDEV void dec(u32 c0, u32, float* w) const {
+    const u32 j = (c0 & 255u) >> 5;
+    u32 sc, mn;
+    k4_scmin(h, j, sc, mn);
+    const float d1 = f16v(h.x & 0xffffu) * (float)sc * ((j & 1u) ? 0.0625f : 1.0f), m1 = f16v(h.x >> 16) * (float)mn;
+    const u32 mask = (j & 1u) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+    const u32 qq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const u32 v = opq(qq[k] & mask);
+#pragma unroll
+      for (int t = 0; t < 4; t++) w[4 * k + t] = __builtin_fmaf(d1, ubyte(v, t), -m1);
+    }
+  }
+};
+
+template <> struct Half<FM_Q5_K> {
+  uint4 h, qh, q;
+  MDEV void ld(const u8* row, u32 c0, u32 jh) {
+    const u8* B = row + (u64)(c0 >> 8) * 176u;
+    const u32 j = (c0 & 255u) >> 5;
+    h = *(const uint4*)B;
+    qh = *(const uint4*)(B + 16 + 16 * jh);
+    q = *(const uint4*)(B + 48 + 32 * (j >> 1) + 16 * jh);
+  }
+  MDEV void dec(u32 c0, u32, float* w) const {
+    const u32 j = (c0 & 255u) >> 5;
+    u32 sc, mn;
+    k4_scmin(h, j, sc, mn);
+    const float d1 = f16v(h.x & 0xffffu) * (float)sc, m1 = f16v(h.x >> 16) * (float)mn;
+    const u32 sh = 4u * (j & 1u);
+    const u32 qq[4] = {q.x, q.y, q.z, q.w}, hh[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const u32 v = opq(((qq[k] >> sh) & 0x0F0F0F0Fu) | (((hh[k] >> j) & 0x01010101u) << 4));
+#pragma unroll
+      for (int t = 0; t < 4; t++) w[4 * k + t] = __builtin_fmaf(d1, ubyte(v, t), -m1);
+    }
+  }
+};
+
+template <> struct Half<FM_Q6_K> {
+  Raw16 ql, qh;
+  u32 scw, d, sl, sh;
+  MDEV void ld(const u8* row, u32 c0, u32 jh) {
+    const u8* B = row + (u64)(c0 >> 8) * 210u;
+    const u32 r = c0 & 255u, n = r >> 7, quad = (r & 127u) >> 5;
+    const u8* pl = B + 64 * n + 32 * (quad & 1u) + 16 * jh;
+    const u8* ph = B + 128 + 32 * n + 16 * jh;
+    sl = ((u32)(uintptr_t)pl & 2u) * 8u;
+    sh = ((u32)(uintptr_t)ph & 2u) * 8u;
+    ql = ld16_a2(pl);
+    qh = ld16_a2(ph);
+    scw = ld_u16(B + 192 + 8 * n + 2 * quad);
+    d = ld_u16(B + 208);
+  }
+  MDEV void dec(u32 c0, u32 jh, float* w) const {
+    const u32 r = c0 & 255u, quad = (r & 127u) >> 5;
+    const float ds = f16v(d) * (float)(int)(signed char)((scw >> (8 * jh)) & 255u);
+    const u32 nsh = quad >= 2u ? 4u : 0u, hsh = 2u * quad;
+    u32 l4[4], h4[4];
+    al16(ql, sl, l4);
+    al16(qh, sh, h4);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const u32 v = opq(((l4[k] >> nsh) & 0x0F0F0F0Fu) | (((h4[k] >> hsh) & 0x03030303u) << 4));
+#pragma unroll
+      for (int t = 0; t < 4; t++) w[4 * k + t] = ds * (ubyte(v, t) - 32.0f);
     }
   }
 };

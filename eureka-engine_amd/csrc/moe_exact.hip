@@ -24,8 +24,13 @@
 __device__ unsigned long long moe_phase_t[64];
 #define PHASE(i) \
   do { if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) moe_phase_t[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+// per-block start / end stamps of kernel k: moe_blk_t[k][block][0 | 1] (blocks < 4096, grid x only)
+__device__ unsigned long long moe_blk_t[4][4096][2];
+#define BSTAMP(k, i) \
+  do { if (threadIdx.x == 0 && blockIdx.x < 4096 && blockIdx.y == 0) moe_blk_t[k][blockIdx.x][i] = __builtin_amdgcn_s_memrealtime(); } while (0)
 #else
 #define PHASE(i) do {} while (0)
+#define BSTAMP(k, i) do {} while (0)
 #endif
 
 // ---------------------------------------------------------------- tree rows (router, shared)
@@ -92,7 +97,9 @@ DEV void tree_body(const TreeArgs& a, u32 bx, u32 t, u32 L) {
 }
 template <u32 NSP>
 __global__ void __launch_bounds__(64) k_tree_rows(TreeArgs a) {
+  BSTAMP(0, 0);
   tree_body<NSP>(a, blockIdx.x, blockIdx.y, threadIdx.x);
+  BSTAMP(0, 1);
 }
 
 // ---------------------------------------------------------------- top-k (llb_moe_topk)
@@ -129,6 +136,13 @@ DEV void wave_amax(float& bv, u32& bi) {
   }
 }
 
+// lanes of one wave exchanging words through LDS: a wave's LDS operations complete in issue order,
+// so only the compiler must not move them across this point
+#define WAVE_SYNC() do { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); __builtin_amdgcn_wave_barrier(); } while (0)
+// LDS of topk_body256 (floats): p [1024], sums / tau / count / lane maxima [128], chosen p [64],
+// candidates [256 + 256], the chosen experts [64] (u32)
+#define TOPK_SIDS (1024 + 128 + 64 + 512)
+#define TOPK_LDS (TOPK_SIDS + 64)
 // one block of 256 a token (ne <= 1024), llb_moe_topk's arithmetic: mx = max; v = exp(l - mx); the
 // sum in the 1024-thread block's order (expert e on thread e: each 32-expert group by the xor tree
 // 16 .. 1, then the group sums in order); p = v (1 / sum). Selection by rank instead of k argmax
@@ -136,7 +150,88 @@ DEV void wave_amax(float& bv, u32& bi) {
 // argmax (ties to the lower index) would take e, so the experts with rank < k are the top k in that
 // order -- independent compares, no serial chain. wt_j = p / max(sum of the k p in rank order,
 // 2^-14); sgo = sigmoid(sg). Thread t holds experts t, t + 256, t + 512, t + 768.
-DEV void topk_body256(const TopkArgs& a, u32 t, float* sm) {
+// the value of lane L ^ J (J a power of two below 64), through DPP / permlane swaps
+template <u32 J> DEV u32 lane_xor(u32 v, u32 L) {
+  if constexpr (J == 1) return dppu<DPP_XOR1>(v);
+  else if constexpr (J == 2) return dppu<DPP_XOR2>(v);
+  else if constexpr (J == 4) {
+    // no select (a select around DPP may become a branch, and DPP reads of lanes switched off by it
+    // return the old operand): banks 0 and 2 of each row (lanes with bit 2 clear) take lane + 4
+    // (row_ror:12), then banks 1 and 3 take lane - 4 (row_ror:4) over that result
+    const u32 up = (u32)__builtin_amdgcn_update_dpp(0, (int)v, DPP_UP4, 0xf, 0x5, false);
+    return (u32)__builtin_amdgcn_update_dpp((int)up, (int)v, 0x124, 0xf, 0xa, false);
+  }
+  else if constexpr (J == 8) return dppu<DPP_XOR8>(v);
+  else if constexpr (J == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (L & 16) ? r[0] : r[1];
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (L & 32) ? r[0] : r[1];
+  }
+}
+// one compare-exchange stage of a bitonic sort over the wave's 64 keys: lane L keeps the larger of
+// its key and lane L ^ J's when (L & J) == 0 matches the block's direction (descending where
+// (L & K) == 0), else the smaller
+template <u32 K, u32 J> DEV u64 bitonic_step(u64 key, u32 L) {
+  const u32 hi = lane_xor<J>((u32)(key >> 32), L), lo = lane_xor<J>((u32)key, L);
+  const u64 other = (u64)hi << 32 | lo;
+  const bool keep_max = ((L & J) == 0) == ((L & K) == 0);
+  const bool gt = other > key;
+  return gt == keep_max ? other : key;
+}
+// 32-bit values: the same network with max / min (no index, for when only values matter)
+template <u32 K, u32 J> DEV u32 bitonic_step32(u32 v, u32 L) {
+  const u32 o = lane_xor<J>(v, L);
+  return (((L & J) == 0) == ((L & K) == 0)) ? max(v, o) : min(v, o);
+}
+DEV u32 wave_sort_desc32(u32 k, u32 L) {
+  k = bitonic_step32<2, 1>(k, L);
+  k = bitonic_step32<4, 2>(k, L);   k = bitonic_step32<4, 1>(k, L);
+  k = bitonic_step32<8, 4>(k, L);   k = bitonic_step32<8, 2>(k, L);   k = bitonic_step32<8, 1>(k, L);
+  k = bitonic_step32<16, 8>(k, L);  k = bitonic_step32<16, 4>(k, L);  k = bitonic_step32<16, 2>(k, L);
+  k = bitonic_step32<16, 1>(k, L);
+  k = bitonic_step32<32, 16>(k, L); k = bitonic_step32<32, 8>(k, L);  k = bitonic_step32<32, 4>(k, L);
+  k = bitonic_step32<32, 2>(k, L);  k = bitonic_step32<32, 1>(k, L);
+  k = bitonic_step32<64, 32>(k, L); k = bitonic_step32<64, 16>(k, L); k = bitonic_step32<64, 8>(k, L);
+  k = bitonic_step32<64, 4>(k, L);  k = bitonic_step32<64, 2>(k, L);  k = bitonic_step32<64, 1>(k, L);
+  return k;
+}
+// the wave's 64 keys sorted descending: lane i holds the i-th largest
+DEV u64 wave_sort_desc(u64 k, u32 L) {
+  k = bitonic_step<2, 1>(k, L);
+  k = bitonic_step<4, 2>(k, L);   k = bitonic_step<4, 1>(k, L);
+  k = bitonic_step<8, 4>(k, L);   k = bitonic_step<8, 2>(k, L);   k = bitonic_step<8, 1>(k, L);
+  k = bitonic_step<16, 8>(k, L);  k = bitonic_step<16, 4>(k, L);  k = bitonic_step<16, 2>(k, L);
+  k = bitonic_step<16, 1>(k, L);
+  k = bitonic_step<32, 16>(k, L); k = bitonic_step<32, 8>(k, L);  k = bitonic_step<32, 4>(k, L);
+  k = bitonic_step<32, 2>(k, L);  k = bitonic_step<32, 1>(k, L);
+  k = bitonic_step<64, 32>(k, L); k = bitonic_step<64, 16>(k, L); k = bitonic_step<64, 8>(k, L);
+  k = bitonic_step<64, 4>(k, L);  k = bitonic_step<64, 2>(k, L);  k = bitonic_step<64, 1>(k, L);
+  return k;
+}
+
+// a token's routing out of topk_body256's LDS into ids / wt / sgo (the renormalised weights as
+// llb_moe_topk: the rank-order sum of the chosen p, clamped at 2^-14, divides each)
+DEV void topk_write(const TopkArgs& a, u32 t, const float* sm) {
+  const u32 tid = threadIdx.x;
+  const float* wv = sm + 1152;
+  const u32* ids = (const u32*)(sm + TOPK_SIDS);
+  if (tid < 64) {
+    float s = 0.0f;
+    for (u32 j = 0; j < a.nk; j++) s = s + wv[j];
+    s = s < 6.103515625e-5f ? 6.103515625e-5f : s;
+    if (tid < a.nk) {
+      a.wt[(u64)t * a.nk + tid] = wv[tid] / s;
+      a.ids[(u64)t * a.nk + tid] = ids[tid];
+    }
+    if (tid == 0) {
+      const float sg = a.has_sg ? a.lg[(u64)t * a.lstride + a.ne] : 0.0f;
+      a.sgo[t] = 1.0f / (1.0f + exp_f(-sg));
+    }
+  }
+}
+DEV void topk_body256(const TopkArgs& a, u32 t, float* sm, bool wr) {
   float* ps = sm;               // [ne] p
   float* red = sm + 1024;       // [32] group sums / wave maxima, [32] tau, [40] count, [64..128) lane maxima
   float* wv = sm + 1152;        // [64] the chosen p by rank, then [256] + [256] candidates
@@ -183,55 +278,64 @@ DEV void topk_body256(const TopkArgs& a, u32 t, float* sm) {
   }
   __syncthreads();
   PHASE(3);
-  // prune: tau = the k-th largest of the 64 strided maxima m_l = max p[l + 64 j]; at least k values
-  // are >= tau, so the k-th largest value is >= tau and every expert of the top k has p >= tau
+  // Selection in wave 0 alone (no block barriers inside). tau = the nk-th largest of the 64 strided
+  // maxima m_l = max p[l + 64 j]: at least nk values are >= tau, so the nk-th largest value is >= tau
+  // and every expert of the top k has p >= tau. The experts with p >= tau (the candidates) are
+  // compacted by ballot and ranked among themselves; ranks below nk are the top k in order. More
+  // than 64 candidates (heavy ties) fall back to a rank over every expert, block-wide.
+  u32* ids = (u32*)(sm + TOPK_SIDS);  // [nk] in LDS; copied out when wr
   u32* cnt = (u32*)(red + 40);
-  float* cv = wv + 64;                 // [256] candidate p
-  u32* ci = (u32*)(cv + 256);          // [256] candidate expert
-  float* lm = red + 64;                // [64] lane maxima (past red's 32 + the counters)
-  if (tid < 64) {
-    float m = ps[tid];
-    for (u32 e = tid + 64; e < a.ne; e += 64) m = fmaxf(m, ps[e]);
-    lm[tid] = tid < a.ne ? m : bits_f(0xFF800000u);
-  }
-  if (tid == 64) *cnt = 0;
-  __syncthreads();
-  {
-    const float m = lm[tid & 63];
-    u32 r = 0;
+  float* cv = wv + 64;                 // [64] candidate p
+  u32* ci = (u32*)(cv + 256);          // [64] candidate expert
+  float* lm = red + 64;                // [64] lane maxima
+  if (w == 0) {
+    // Order keys: (bits of p) << 32 | ~e. p >= 0, so its bits order like p; a larger key is a larger
+    // p, then a lower index. -inf (and NaN) map to key 0, below every real p. The 64 lane maxima and
+    // then the (at most 64) candidates are ranked by a bitonic sort across the wave.
+    u64* kk = (u64*)cv;  // [64] candidate keys
+    if (L < a.nk) ids[L] = 0;  // a valid expert whatever happens below (NaN logits rank nothing)
+    const u32 nj = (a.ne + 63) / 64;
+    float pv[16];
 #pragma unroll
-    for (u32 q = 16 * w; q < 16 * w + 16; q++) r += (lm[q] > m || (lm[q] == m && q < (tid & 63)));
-    ((u32*)cv)[tid] = r;               // partial ranks, reused below
-  }
-  __syncthreads();
-  if (tid < 64) {
-    const u32* pr = (const u32*)cv;
-    const u32 r = pr[tid] + pr[tid + 64] + pr[tid + 128] + pr[tid + 192];
-    if (r == a.nk - 1) red[32] = lm[tid];
-  }
-  __syncthreads();
-  const float tau = red[32];
+    for (u32 j = 0; j < 16; j++) pv[j] = (j < nj && L + 64 * j < a.ne) ? ps[L + 64 * j] : -1.0f;  // p >= 0
+    float m = pv[0];
 #pragma unroll
-  for (u32 i = 0; i < 4; i++) {
-    const u32 e = tid + 256 * i;
-    if (i < ni && e < a.ne && p[i] >= tau) {
-      const u32 s = atomicAdd(cnt, 1u);
-      if (s < 256) { cv[s] = p[i]; ci[s] = e; }
+    for (u32 j = 1; j < 16; j++)
+      if (j < nj) m = fmaxf(m, pv[j]);
+    // tau needs only the value of the nk-th largest lane maximum: sort the bits (p >= 0 orders
+    // like its bits; -inf lanes as 0)
+    const u32 mb = (L < a.ne && m >= 0.0f) ? __float_as_uint(m) : 0u;
+    PHASE(40);
+    const u32 sb = wave_sort_desc32(mb, L);
+    const float tau = __uint_as_float((u32)__builtin_amdgcn_readlane((int)sb, (int)(a.nk - 1)));
+    kk[L] = 0ull;
+    WAVE_SYNC();
+    PHASE(41);
+    u32 base = 0;
+#pragma unroll
+    for (u32 j = 0; j < 16; j++) {
+      if (j < nj) {
+        const bool c = pv[j] >= tau;  // -1 (past ne) never is
+        const u64 bal = __ballot(c);
+        const u32 pos = base + __builtin_amdgcn_mbcnt_hi((u32)(bal >> 32), __builtin_amdgcn_mbcnt_lo((u32)bal, 0u));
+        if (c && pos < 64) kk[pos] = ((u64)__float_as_uint(pv[j]) << 32) | (0xFFFFFFFFu - (L + 64 * j));
+        base += (u32)__popcll(bal);
+      }
     }
+    WAVE_SYNC();
+    PHASE(42);
+    if (base <= 64) {
+      const u64 ck = wave_sort_desc(kk[L], L);  // zero keys (no candidate) sort last
+      if (L < a.nk && ck != 0ull) {  // a zero key is no candidate: the slot keeps expert 0
+        ids[L] = 0xFFFFFFFFu - (u32)ck;
+        wv[L] = __uint_as_float((u32)(ck >> 32));
+      }
+    }
+    PHASE(43);
+    if (L == 0) *cnt = base;
   }
   __syncthreads();
-  const u32 nc = *cnt;
-  u32* ids = a.ids + (u64)t * a.nk;
-  if (nc <= 256) {
-    // rank among the candidates (all of the top k are among them, so ranks below k agree)
-    if (tid < nc) {
-      const float v = cv[tid];
-      const u32 me = ci[tid];
-      u32 r = 0;
-      for (u32 q = 0; q < nc; q++) r += (cv[q] > v || (cv[q] == v && ci[q] < me));
-      if (r < a.nk) { ids[r] = me; wv[r] = v; }
-    }
-  } else {
+  if (*cnt > 64) {
     // heavy ties: rank over every expert
     u32 rk[4] = {0, 0, 0, 0};
     for (u32 q = 0; q < a.ne; q++) {
@@ -247,22 +351,13 @@ DEV void topk_body256(const TopkArgs& a, u32 t, float* sm) {
   }
   __syncthreads();
   PHASE(4);
-  if (tid < 64) {
-    float s = 0.0f;
-    for (u32 j = 0; j < a.nk; j++) s = s + wv[j];
-    s = s < 6.103515625e-5f ? 6.103515625e-5f : s;
-    if (tid < a.nk) a.wt[(u64)t * a.nk + tid] = wv[tid] / s;
-    if (tid == 0) {
-      const float sg = a.has_sg ? lg[a.ne] : 0.0f;
-      a.sgo[t] = 1.0f / (1.0f + exp_f(-sg));
-    }
-  }
+  if (wr) topk_write(a, t, sm);
   PHASE(5);
 }
 
 __global__ void __launch_bounds__(256) k_topk(TopkArgs a) {
-  __shared__ float sm[1024 + 128 + 64 + 512];
-  topk_body256(a, blockIdx.x, sm);
+  __shared__ float sm[TOPK_LDS];
+  topk_body256(a, blockIdx.x, sm, true);
 }
 
 // ---------------------------------------------------------------- stride rows (experts)
@@ -353,6 +448,94 @@ __global__ void __launch_bounds__(256) k_gu_exact(GuArgs a, u32 np) {
   gu_body<FG, FU>(a, np, blockIdx.x, sm);
 }
 
+// ---- 8 lanes a row: llb_gemv_any's stride order with the partial sums in registers.
+// Lane q of a row's 8 (c0 = q & 3, jh = q >> 2) holds virtual lanes v = 8 c0 + 4 jh + i (i < 4) of
+// the 32-lane order: v sums leaves v, v + 32, v + 64, ... in turn, and leaf v + 32 m is leaf
+// 4 jh + i of span c0 + 4 m. The xor tree's level 16 pairs lanes q ^ 2, level 8 q ^ 1, level 4 q
+// and q + 4; levels 2 and 1 are inside the lane. The row's dot ends on lane q = 0.
+DEV float fin8(float* acc) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) acc[i] = xadd2(acc[i]);
+#pragma unroll
+  for (int i = 0; i < 4; i++) acc[i] = xadd1(acc[i]);
+#pragma unroll
+  for (int i = 0; i < 4; i++) acc[i] = xadd4(acc[i]);
+  return (acc[0] + acc[2]) + (acc[1] + acc[3]);
+}
+template <u32 F> DEV void acc16(const Half<F>& h, u32 c, u32 jh, const float* xs, float* acc) {
+  float w[16];
+  h.dec(32 * c, jh, w);
+  const float4* xp = (const float4*)(xs + 32 * c + 16 * jh);
+#pragma unroll
+  for (int i = 0; i < 4; i++) acc[i] = acc[i] + leaf4(w + 4 * i, xp[i]);
+}
+// NM spans a lane (cols = 128 NM), every raw load in flight before the caller waits for x
+template <u32 F, u32 NM> struct Row8 {
+  Half<F> h[NM];
+  MDEV void ld(const u8* row, u32 q) {
+#pragma unroll
+    for (u32 m = 0; m < NM; m++) h[m].ld(row, 32 * ((q & 3) + 4 * m), q >> 2);
+  }
+  MDEV float dot(const float* xs, u32 q) const {
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (u32 m = 0; m < NM; m++) acc16<F>(h[m], (q & 3) + 4 * m, q >> 2, xs, acc);
+    return fin8(acc);
+  }
+};
+// any cols (a multiple of 128): loads in the loop
+template <u32 F> DEV float row8_dot(const u8* row, const float* xs, u32 cols, u32 q) {
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+  for (u32 m = 0; m < cols / 128; m++) {
+    Half<F> h;
+    h.ld(row, 32 * ((q & 3) + 4 * m), q >> 2);
+    acc16<F>(h, (q & 3) + 4 * m, q >> 2, xs, acc);
+  }
+  return fin8(acc);
+}
+
+// gate + up + SwiGLU, 8 lanes a row: a block is 16 act rows of one slot (32 groups of 8 lanes, gate
+// row on even groups, up row on odd ones, so lane 16 k + 8 holds the up dot of lane 16 k's gate row).
+// Gate and up in one format.
+template <u32 F, u32 NM>
+__global__ void __launch_bounds__(256) k_gu_lane(GuArgs a) {
+  extern __shared__ float xs[];  // [dm]
+  PHASE(8);
+  BSTAMP(2, 0);
+  const u32 tid = threadIdx.x, gi = tid >> 3, q = tid & 7;
+  const u32 task0 = blockIdx.x * 16, slot = task0 / a.ef, r = task0 % a.ef + (gi >> 1);
+  const float* x = a.h2 + (u64)(slot / a.nk) * a.dm;
+  const u64 e = a.ids[slot];
+  const u8* row = (gi & 1) ? a.U + e * a.es + (u64)r * a.rbu : a.G + e * a.es + (u64)r * a.rbg;
+  float s;
+  if constexpr (NM != 0) {
+    // issue order matters (vmcnt retires in order): x first, then the weights, so x reaches LDS
+    // while the weights are still in flight
+    static_assert(NM == 16, "x staging is written for dm = 2048: two float4 a thread");
+    const float4 xv0 = ((const float4*)x)[tid], xv1 = ((const float4*)x)[tid + 256];
+    __asm__ volatile("" ::: "memory");
+    Row8<F, NM> w;
+    w.ld(row, q);
+    __asm__ volatile("" ::: "memory");
+    PHASE(9);
+    ((float4*)xs)[tid] = xv0;
+    ((float4*)xs)[tid + 256] = xv1;
+    __syncthreads();
+    PHASE(10);
+    s = w.dot(xs, q);
+    PHASE(11);
+  } else {
+    for (u32 i = tid; i < a.dm / 4; i += 256) ((float4*)xs)[i] = ((const float4*)x)[i];
+    __syncthreads();
+    s = row8_dot<F>(row, xs, a.dm, q);
+  }
+  const float u = dppf<DPP_XOR8>(s);
+  if ((tid & 15) == 0) a.act[(u64)slot * a.ef + r] = silu_mul(s, u);
+  PHASE(12);
+  BSTAMP(2, 1);
+}
+
 // down + rank-order combine + gated shared expert + residual (llb_moe_dn): rw rows of one token a
 // block; task j < nk is routed expert ids[j]'s row against act_j, j = nk the shared expert's down
 // row against sa (computed here from the shared gate / up logits)
@@ -427,6 +610,135 @@ __global__ void __launch_bounds__(256) k_dn_exact(DnArgs a) {
   dn_body<FD, FS>(a, blockIdx.x, blockIdx.y, sm);
 }
 
+// top-k + gate + up + SwiGLU in one launch: each block recomputes its token's routing (the same
+// topk_body256 as k_topk, so the same ids and weights) instead of reading ids written by a previous
+// launch; the first block of each token writes ids / wt / sgo for the down kernel. Rows as k_gu_lane.
+template <u32 F, u32 NM>
+__global__ void __launch_bounds__(256) k_gu_topk(GuArgs a, TopkArgs k) {
+  extern __shared__ float sm[];  // [TOPK_LDS] routing, then [dm] x
+  float* xs = sm + TOPK_LDS;
+  PHASE(8);
+  BSTAMP(2, 0);
+  const u32 tid = threadIdx.x, gi = tid >> 3, q = tid & 7;
+  const u32 task0 = blockIdx.x * 16, slot = task0 / a.ef, r = task0 % a.ef + (gi >> 1);
+  const u32 t = slot / a.nk, jr = slot % a.nk;
+  const float* x = a.h2 + (u64)t * a.dm;
+  float s;
+  if constexpr (NM != 0) {
+    static_assert(NM == 16, "x staging is written for dm = 2048: two float4 a thread");
+    // x is loaded first (vmcnt retires in order) and reaches LDS once the routing is done
+    const float4 xv0 = ((const float4*)x)[tid], xv1 = ((const float4*)x)[tid + 256];
+    topk_body256(k, t, sm, false);
+    const u64 e = ((const u32*)(sm + TOPK_SIDS))[jr];
+    const u8* row = (gi & 1) ? a.U + e * a.es + (u64)r * a.rbu : a.G + e * a.es + (u64)r * a.rbg;
+    Row8<F, NM> w;
+    w.ld(row, q);
+    __asm__ volatile("" ::: "memory");
+    if (task0 % a.ef == 0 && jr == 0) topk_write(k, t, sm);  // once a token, behind the weight loads
+    PHASE(9);
+    ((float4*)xs)[tid] = xv0;
+    ((float4*)xs)[tid + 256] = xv1;
+    __syncthreads();
+    PHASE(10);
+    s = w.dot(xs, q);
+    PHASE(11);
+  } else {
+    topk_body256(k, t, sm, task0 % a.ef == 0 && jr == 0);
+    const u64 e = ((const u32*)(sm + TOPK_SIDS))[jr];
+    const u8* row = (gi & 1) ? a.U + e * a.es + (u64)r * a.rbu : a.G + e * a.es + (u64)r * a.rbg;
+    for (u32 i = tid; i < a.dm / 4; i += 256) ((float4*)xs)[i] = ((const float4*)x)[i];
+    __syncthreads();
+    s = row8_dot<F>(row, xs, a.dm, q);
+  }
+  const float u = dppf<DPP_XOR8>(s);
+  if ((tid & 15) == 0) a.act[(u64)slot * a.ef + r] = silu_mul(s, u);
+  PHASE(12);
+  BSTAMP(2, 1);
+}
+
+// down + rank-order combine + gated shared expert + residual, 8 lanes a row. A block takes R
+// outputs of one token and their nt = nk (+ 1 shared) row dots: task k = j R + rl (expert-major, so
+// a wave's groups share one act row and read neighbouring weight rows), tasks gi and gi + 32 of
+// the block's 32 groups (R nt <= 64). The shared down row has the routed rows' format and width
+// (ef = sf = 128 NM).
+//
+// Issue order matters (vmcnt retires in order): ids, then act and the shared gate / up logits into
+// registers, then the weights; act / sa reach LDS while the weights are in flight. The code around
+// the loads is straight-line (per-lane branches make the compiler wait at the joins): tasks past
+// the end load a valid row and are dropped, and staging steps past the end re-copy a word another
+// thread copies too (index min(tid + 256 i, n - 256 + tid), n >= 256).
+template <u32 F, u32 HS, u32 NM>
+__global__ void __launch_bounds__(256) k_dn_lane(DnArgs a, u32 R) {
+  extern __shared__ float sm[];
+  BSTAMP(3, 0);
+  PHASE(16);
+  const u32 nt = a.nk + HS, ntask = R * nt;
+  float* xa = sm;                        // [nk][ef] act of the token's slots
+  float* sa = xa + a.nk * a.ef;          // [sf]
+  float* part = sa + (HS ? a.sf : 0u);   // [R][nt]
+  const u32 t = blockIdx.y, r0 = blockIdx.x * R;
+  const u32 tid = threadIdx.x, gi = tid >> 3, q = tid & 7;
+  u32 kind[2], eid[2];  // kind 0 none, 1 routed, 2 shared
+#pragma unroll
+  for (u32 p = 0; p < 2; p++) {
+    const u32 k = gi + 32 * p, j = k / R, r = r0 + k % R;
+    kind[p] = (k < ntask && r < a.dm) ? (j < a.nk ? 1u : 2u) : 0u;
+    eid[p] = a.ids[(u64)t * a.nk + min(j, a.nk - 1)];
+  }
+  const float4* act4 = (const float4*)(a.act + (u64)t * a.nk * a.ef);
+  const u32 na4 = a.nk * a.ef / 4;  // 256 .. 2048
+  // (separate variables, not arrays: the ordering fences below would keep an array in memory)
+#define DN_AI(i) min(tid + 256u * (i), na4 - 256u + tid)
+  const float4 av0 = act4[DN_AI(0)], av1 = act4[DN_AI(1)], av2 = act4[DN_AI(2)], av3 = act4[DN_AI(3)];
+  const float4 av4 = act4[DN_AI(4)], av5 = act4[DN_AI(5)], av6 = act4[DN_AI(6)], av7 = act4[DN_AI(7)];
+  float gg0 = 0.0f, gg1 = 0.0f, gu0 = 0.0f, gu1 = 0.0f;  // sf 256 or 512
+  const u32 sc0 = min(tid, a.sf - 256u + tid), sc1 = min(tid + 256u, a.sf - 256u + tid);
+  if (HS) {
+    const float* g = a.gsu + (u64)t * 2 * a.sf;
+    gg0 = g[sc0]; gg1 = g[sc1]; gu0 = g[a.sf + sc0]; gu1 = g[a.sf + sc1];
+  }
+  // the scheduler may not move the weight loads above the staging loads, nor the LDS stores above them
+  __asm__ volatile("" ::: "memory");
+  Row8<F, NM> w[2];
+#pragma unroll
+  for (u32 p = 0; p < 2; p++) {
+    const u32 k = gi + 32 * p, r = min(r0 + k % R, a.dm - 1);
+    const u8* drow = a.D + ((u64)eid[p] * a.dm + r) * a.rbd;
+    w[p].ld(HS && kind[p] == 2 ? a.SD + (u64)r * a.rbs : drow, q);
+  }
+  __asm__ volatile("" ::: "memory");
+  PHASE(17);
+  float4* xa4 = (float4*)xa;
+  xa4[DN_AI(0)] = av0; xa4[DN_AI(1)] = av1; xa4[DN_AI(2)] = av2; xa4[DN_AI(3)] = av3;
+  xa4[DN_AI(4)] = av4; xa4[DN_AI(5)] = av5; xa4[DN_AI(6)] = av6; xa4[DN_AI(7)] = av7;
+#undef DN_AI
+  if (HS) {
+    sa[sc0] = silu_mul(gg0, gu0);
+    sa[sc1] = silu_mul(gg1, gu1);
+  }
+  __syncthreads();
+  PHASE(18);
+#pragma unroll
+  for (u32 p = 0; p < 2; p++) {
+    const u32 k = gi + 32 * p, j = k / R, rl = k % R;
+    const float s = w[p].dot(kind[p] == 2 ? sa : xa + min(j, a.nk - 1) * a.ef, q);
+    if (kind[p] && q == 0) part[rl * nt + j] = s;
+  }
+  __syncthreads();
+  PHASE(19);
+  if (tid < R && r0 + tid < a.dm) {
+    const u32 r = r0 + tid;
+    const float* wt = a.wt + (u64)t * a.nk;
+    const float* pr = part + tid * nt;
+    float mo = 0.0f;
+    for (u32 j = 0; j < a.nk; j++) mo = j == 0 ? pr[0] * wt[0] : mo + pr[j] * wt[j];
+    const float res = a.x1 ? a.x1[(u64)t * a.dm + r] : 0.0f;
+    a.y[(u64)t * a.dm + r] = HS ? (mo + pr[a.nk] * a.sgo[t]) + res : mo + res;
+  }
+  PHASE(20);
+  BSTAMP(3, 1);
+}
+
 // ---------------------------------------------------------------- the fused decode layer
 //
 // One persistent launch runs a whole layer. Blocks take work items from a ticket counter in a
@@ -491,7 +803,7 @@ __global__ void __launch_bounds__(256) k_fused(FusedArgs f) {
       item_done(&c[1]);
     } else if (it < e2) {
       phase_wait(&c[1], f.nR, &c[5], f.spin);
-      topk_body256(f.tk, it - e1, sm);
+      topk_body256(f.tk, it - e1, sm, true);
       item_done(&c[2]);
     } else if (it < e3) {
       phase_wait(&c[2], nK, &c[5], f.spin);
@@ -545,12 +857,30 @@ int launch_topk(const TopkArgs& a, u32 T, hipStream_t st) {
 }
 
 int launch_gu_exact(const GuArgs& a, u32 fg, u32 fu, u32 nslots, hipStream_t st) {
-  if (fg != fu) return -1;
-  const u32 np = 4;  // 8 rows a block: at dm 2048 each thread decodes one span of 2 rows
-  dim3 grid(nslots * a.ef / np);
-  const size_t sm = ((size_t)a.dm + (size_t)2 * np * (a.dm / 4)) * 4;
+  if (fg != fu || a.ef % 16 || a.dm % 128) return -1;
+  const dim3 grid(nslots * a.ef / 16);
+  const size_t sm = (size_t)a.dm * 4;
 #define GU_L(F) \
-  if (fg == F) { hipLaunchKernelGGL((k_gu_exact<F, F>), grid, dim3(256), sm, st, a, np); return 0; }
+  if (fg == F) { \
+    if (a.dm == 2048) hipLaunchKernelGGL((k_gu_lane<F, 16>), grid, dim3(256), sm, st, a); \
+    else hipLaunchKernelGGL((k_gu_lane<F, 0>), grid, dim3(256), sm, st, a); \
+    return 0; \
+  }
+  FM_CASES(GU_L)
+#undef GU_L
+  return -1;
+}
+
+int launch_gu_topk(const GuArgs& a, const TopkArgs& k, u32 fg, u32 fu, u32 nslots, hipStream_t st) {
+  if (fg != fu || a.ef % 16 || a.dm % 128 || k.ne > 1024 || k.nk > 64) return -1;
+  const dim3 grid(nslots * a.ef / 16);
+  const size_t sm = ((size_t)TOPK_LDS + a.dm) * 4;
+#define GU_L(F) \
+  if (fg == F) { \
+    if (a.dm == 2048) hipLaunchKernelGGL((k_gu_topk<F, 16>), grid, dim3(256), sm, st, a, k); \
+    else hipLaunchKernelGGL((k_gu_topk<F, 0>), grid, dim3(256), sm, st, a, k); \
+    return 0; \
+  }
   FM_CASES(GU_L)
 #undef GU_L
   return -1;
@@ -563,8 +893,27 @@ u32 dn_rows(u32 nk, u32 ef, u32 sf) {
 }
 
 int launch_dn_exact(const DnArgs& a, u32 fd, u32 fs, u32 T, hipStream_t st) {
-  dim3 grid((a.dm + a.rw - 1) / a.rw, T);
   const u32 nt = a.nk + (fs ? 1u : 0u);
+  const u32 R = 64 / nt;  // outputs a block: R nt row dots in two passes of 32 groups
+  const u32 nm = a.ef / 128;
+  const bool lane = R >= 1 && (fs == 0 || (fs == fd && a.sf == a.ef)) && a.ef % 128 == 0 &&
+                    (nm == 2 || nm == 4 || nm == 6 || nm == 8) && a.nk * a.ef >= 1024 && a.nk * a.ef <= 8192;
+  if (lane) {
+    const size_t lsm = ((size_t)a.nk * a.ef + (fs ? a.sf : 0) + (size_t)R * nt) * 4;
+    const dim3 grid((a.dm + R - 1) / R, T);
+#define DN_N(F, HS, N) \
+  if (nm == N) { hipLaunchKernelGGL((k_dn_lane<F, HS, N>), grid, dim3(256), lsm, st, a, R); return 0; }
+#define DN_L(F) \
+  if (fd == F) { \
+    if (fs) { DN_N(F, 1, 2) DN_N(F, 1, 4) DN_N(F, 1, 6) DN_N(F, 1, 8) } \
+    else { DN_N(F, 0, 2) DN_N(F, 0, 4) DN_N(F, 0, 6) DN_N(F, 0, 8) } \
+  }
+    FM_CASES(DN_L)
+#undef DN_L
+#undef DN_N
+    return -1;
+  }
+  dim3 grid((a.dm + a.rw - 1) / a.rw, T);
   const size_t sm = ((size_t)a.rw * (a.nk * a.ef / 4 + (fs ? a.sf / 4 : 0)) + (fs ? a.sf : 0) + a.rw * nt) * 4;
 #define DN_L(FD, FS) \
   if (fd == FD && fs == FS) { hipLaunchKernelGGL((k_dn_exact<FD, FS>), grid, dim3(256), sm, st, a); return 0; }
@@ -584,7 +933,7 @@ size_t fused_lds(const FusedArgs& f) {
   const size_t gu = ((size_t)f.gu.dm + (size_t)2 * f.np * (f.gu.dm / 4)) * 4;
   const u32 nt = f.dn.nk + (f.dn.sf ? 1u : 0u);
   const size_t dn = ((size_t)f.dn.rw * (f.dn.nk * f.dn.ef / 4 + f.dn.sf / 4) + f.dn.sf + f.dn.rw * nt) * 4;
-  const size_t tk = (size_t)(1024 + 128 + 64 + 512) * 4;  // topk_body256's LDS
+  const size_t tk = (size_t)TOPK_LDS * 4;  // topk_body256's LDS
   const size_t m = gu > dn ? gu : dn;
   return m > tk ? m : tk;
 }

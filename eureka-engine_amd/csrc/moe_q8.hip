@@ -140,7 +140,7 @@ template <> __device__ __forceinline__ float blk_q8<FM_Q6_K>(const u8* row, u32 
 }
 template <> __device__ __forceinline__ float blk_q8<FM_Q8_0>(const u8* row, u32 b, const u32* xq, float2 e) {
   const u8* B = row + (u64)b * 34u;
-  const u32* a = (const u32*)((uintptr_t)B & ~(uintptr_t)3);
+  const u32* a = al4(B);
   const bool odd = ((uintptr_t)B & 2u) != 0;
   u32 v[9];
 #pragma unroll

@@ -89,6 +89,8 @@ def ref_lib():
 
 
 def ptr(a):
+    """The address of a (None for None). The caller must hold a for as long as the address is used:
+    ptr(temporary) can dangle before the call that receives it runs."""
     return a.ctypes.data if a is not None else None
 
 
@@ -183,8 +185,9 @@ class HostLayer:
         s = self.shape
         T = h2.shape[0]
         y = np.zeros((T, s.dm), np.float64)
-        assert lib().mo_moe_f64(C.byref(self.desc), T, ptr(np.ascontiguousarray(h2, np.float32)),
-                                ptr(np.ascontiguousarray(ids, np.uint32)), ptr(y)) == 0
+        h2c = np.ascontiguousarray(h2, np.float32)  # held while the oracle reads them
+        idc = np.ascontiguousarray(ids, np.uint32)
+        assert lib().mo_moe_f64(C.byref(self.desc), T, ptr(h2c), ptr(idc), ptr(y)) == 0
         return y
 
 

@@ -119,11 +119,49 @@ def test_topk_kernel_ties_and_full(dev):
     gw = dev.read(wt, (3, nk), np.float32)
     for t in range(3):
         ri, rw, rs = np.zeros(nk, np.uint32), np.zeros(nk, np.float32), np.zeros(1, np.float32)
-        ol.lib().mo_topk(ol.ptr(lg[t].copy()), ne, nk, float(lg[t, ne]), ol.ptr(ri), ol.ptr(rw), ol.ptr(rs))
+        row = lg[t].copy()  # held: ctypes gets only its address
+        ol.lib().mo_topk(ol.ptr(row), ne, nk, float(lg[t, ne]), ol.ptr(ri), ol.ptr(rw), ol.ptr(rs))
         assert np.array_equal(gi[t], ri)
         assert np.array_equal(gw[t].view(np.uint32), rw.view(np.uint32))
     assert list(gi[0]) == list(range(nk))
     assert list(gi[1]) == [6, 13, 20, 27, 34]
+
+
+@pytest.mark.parametrize("ne,nk", [(256, 8), (1024, 63), (64, 1), (1000, 10), (513, 5), (130, 64)])
+def test_topk_kernel_patterns(dev, ne, nk):
+    """Tie patterns around the kernel's candidate pruning (the nk-th largest of 64 strided maxima):
+    normal logits, coarse rounding (many ties), all equal, exactly 64 and 65 experts tied at the top,
+    a tie exactly at rank nk - 1 / nk, and one large logit among equal ones."""
+    rng = np.random.default_rng(ne * 100 + nk)
+    rows = [rng.standard_normal(ne), np.round(rng.standard_normal(ne) * 2) / 2, np.zeros(ne)]
+    for ntop in (64, 65):
+        r = rng.standard_normal(ne) - 10.0
+        r[rng.permutation(ne)[:min(ntop, ne)]] = 3.0
+        rows.append(r)
+    r = np.sort(rng.standard_normal(ne))[::-1].copy()
+    if nk < ne:
+        r[nk - 1] = r[nk]  # a tie across the rank-nk boundary
+    rows.append(rng.permutation(r))
+    r = np.zeros(ne)
+    r[ne // 2] = 5.0
+    rows.append(r)
+    T = len(rows)
+    lg = np.zeros((T, ne + 1), np.float32)
+    lg[:, :ne] = np.stack(rows)
+    lg[:, ne] = rng.standard_normal(T)
+    p = dev.upload(lg)
+    ids, wt, sgo = dev.alloc(T * nk * 4), dev.alloc(T * nk * 4), dev.alloc(T * 4)
+    dev.check(dev.lib.llb_moe_hip_topk(p, ne + 1, T, ne, nk, 1, ids, wt, sgo))
+    gi = dev.read(ids, (T, nk), np.uint32)
+    gw = dev.read(wt, (T, nk), np.float32)
+    gs = dev.read(sgo, (T,), np.float32)
+    for t in range(T):
+        ri, rw, rs = np.zeros(nk, np.uint32), np.zeros(nk, np.float32), np.zeros(1, np.float32)
+        row = lg[t].copy()  # held: ctypes gets only its address
+        ol.lib().mo_topk(ol.ptr(row), ne, nk, float(lg[t, ne]), ol.ptr(ri), ol.ptr(rw), ol.ptr(rs))
+        assert np.array_equal(gi[t], ri), (t, gi[t], ri)
+        assert np.array_equal(gw[t].view(np.uint32), rw.view(np.uint32)), t
+        assert gs[t].view(np.uint32) == rs[0].view(np.uint32), t
 
 
 @pytest.mark.parametrize("T,nk,ne", [(1, 8, 256), (64, 8, 128), (2048, 8, 128), (513, 10, 512)])

@@ -194,7 +194,8 @@ def test_tuned_predicate_follows_llb_tuned():
 def _topk(lg, nk, sg=0.0):
     ne = lg.size
     ids, wt, sgo = np.zeros(nk, np.uint32), np.zeros(nk, np.float32), np.zeros(1, np.float32)
-    lib.mo_topk(ol.ptr(np.ascontiguousarray(lg, np.float32)), ne, nk, float(sg), ol.ptr(ids), ol.ptr(wt), ol.ptr(sgo))
+    lgc = np.ascontiguousarray(lg, np.float32)  # held while the oracle reads it
+    lib.mo_topk(ol.ptr(lgc), ne, nk, float(sg), ol.ptr(ids), ol.ptr(wt), ol.ptr(sgo))
     return ids, wt, sgo[0]
 
 
