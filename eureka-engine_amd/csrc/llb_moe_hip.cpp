@@ -540,7 +540,8 @@ static int fused_forward(const llb_moe_layer* L, uint32_t T, const float* h2, co
   f.dn.x1 = x1;
   f.dn.y = y;
   f.T = T;
-  f.rpt = (rows + 7) / 8;
+  const uint32_t rpi = 4 * tree_rows_per_wave(1u << (cdepth(L->dm) - 9));  // 4 waves an item
+  f.rpt = (rows + rpi - 1) / rpi;
   f.nR = T * f.rpt;
   f.np = 4;
   f.nG = T * L->nk * L->ef / f.np;

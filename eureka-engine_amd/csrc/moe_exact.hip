@@ -35,22 +35,9 @@ __device__ unsigned long long moe_blk_t[4][4096][2];
 
 // ---------------------------------------------------------------- tree rows (router, shared)
 
-template <u32 NSP>
-DEV float tree_row_lane(const float* w, const float4* xv) {
-  float s[NSP];
-#pragma unroll
-  for (u32 q = 0; q < NSP; q++) {
-    float l[8];
-#pragma unroll
-    for (u32 g = 0; g < 8; g++) l[g] = leaf4(w + 32 * q + 4 * g, xv[8 * q + g]);
-    s[q] = ((l[0] + l[1]) + (l[2] + l[3])) + ((l[4] + l[5]) + (l[6] + l[7]));
-  }
-#pragma unroll
-  for (u32 st = 1; st < NSP; st <<= 1)
-#pragma unroll
-    for (u32 q = 0; q < NSP; q += 2 * st) s[q] = s[q] + s[q + st];
-  return s[0];
-}
+// lanes of one wave exchanging words through LDS: a wave's LDS operations complete in issue order,
+// so only the compiler must not move them across this point
+#define WAVE_SYNC() do { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); __builtin_amdgcn_wave_barrier(); } while (0)
 
 DEV void span_any(u32 fm, const u8* rp, u32 c0, float* w) {
   switch (fm) {
@@ -61,44 +48,103 @@ DEV void span_any(u32 fm, const u8* rp, u32 c0, float* w) {
   }
 }
 
-#define TREE_RPW 2  // rows a wave: the lane's x span is loaded once for them
+// rows a wave: the lane's x span is loaded once for them, every row's loads in flight together
+// (2 spans of weights a lane at most)
+template <u32 NSP> constexpr u32 tree_rpw() { return NSP >= 2 ? 1u : 2u; }
+u32 tree_rows_per_wave(u32 nsp) { return nsp >= 2 ? 1u : 2u; }
 
 // every tree row of the layer in one launch (router, shared gate logit, shared gate, shared up):
-// a wave takes TREE_RPW consecutive rows (of the concatenated segments), lane L the contiguous
-// leaves [L S, L S + S); blockDim 64, grid (ceil(rows / TREE_RPW), T)
-template <u32 NSP>
-DEV void tree_body(const TreeArgs& a, u32 bx, u32 t, u32 L) {
-  PHASE(24);
-  const u32 c0 = 32 * NSP * L;
-  const bool live = c0 < a.cols;  // pad leaves past cols count +0
-  float4 xv[8 * NSP];
-  const float* x = a.x + (u64)t * a.xstride;
+// a wave takes tree_rpw<NSP>() consecutive rows (of the concatenated segments); blockDim 64, grid
+// (ceil(rows / tree_rpw<NSP>()), T). The tree has 64 NQ leaves (NQ = 8 NSP), leaf i = columns
+// 4 i .. 4 i + 3 (+0 past cols).
+//  * F32 rows (router, shared gate logit) load coalesced: lane L holds leaves 64 q + L (q < NQ);
+//    the tree's first six levels pair lanes (tree64_asc, exact on lane 0), the rest pair q in the lane.
+//  * quantized rows decode whole spans: lane L holds the contiguous leaves [NQ L, NQ L + NQ); the
+//    first log2 NQ levels are in the lane, the last six across lanes.
+// x is loaded coalesced and reaches the second layout through LDS (lanes padded 4 floats apart).
+// The rows' segments are looked up first, then all their loads go out, then each row is reduced.
+template <u32 NQ> DEV float tree_in_lane(float* n) {
 #pragma unroll
-  for (u32 q = 0; q < 8 * NSP; q++) xv[q] = live ? ((const float4*)(x + c0))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-  for (u32 k = 0; k < TREE_RPW; k++) {
-    u32 row = bx * TREE_RPW + k, sgi = 0;
-    while (sgi < a.nseg && row >= a.seg[sgi].rows) { row -= a.seg[sgi].rows; sgi++; }
-    if (sgi >= a.nseg) return;
-    const TreeSeg& sg = a.seg[sgi];
-    float w[32 * NSP];
+  for (u32 st = 1; st < NQ; st <<= 1)
 #pragma unroll
-    for (u32 q = 0; q < NSP; q++) {
-      if (live) span_any(sg.fm, sg.W + (u64)row * sg.rb, c0 + 32 * q, w + 32 * q);
-      else
-#pragma unroll
-        for (u32 i = 0; i < 32; i++) w[32 * q + i] = 0.0f;
-    }
-    PHASE(25 + 2 * k);
-    float v = live ? tree_row_lane<NSP>(w, xv) : 0.0f;  // a dead lane's leaves are all +0 pads
-    v = tree64_asc(v);
-    if (L == 0) sg.out[(u64)t * sg.ostride + row] = sg.bias ? v + sg.bias[row] : v;
-    PHASE(26 + 2 * k);
-  }
+    for (u32 q = 0; q < NQ; q += 2 * st) n[q] = n[q] + n[q + st];
+  return n[0];
 }
 template <u32 NSP>
+DEV void tree_body(const TreeArgs& a, u32 bx, u32 t, u32 L, float* xsh) {
+  PHASE(24);
+  constexpr u32 RPW = tree_rpw<NSP>(), NQ = 8 * NSP, LS = 4 * NQ + 4;
+  const u32 nl4 = a.cols / 4;
+  const float4* x4 = (const float4*)(a.x + (u64)t * a.xstride);
+  float4 xc[NQ];
+#pragma unroll
+  for (u32 q = 0; q < NQ; q++) xc[q] = 64 * q + L < nl4 ? x4[64 * q + L] : make_float4(0.f, 0.f, 0.f, 0.f);
+  u32 row[RPW], sgi[RPW];
+#pragma unroll
+  for (u32 k = 0; k < RPW; k++) {
+    u32 r = bx * RPW + k, s = 0;
+    while (s < a.nseg && r >= a.seg[s].rows) { r -= a.seg[s].rows; s++; }
+    row[k] = r;
+    sgi[k] = s;  // nseg: past the last row
+  }
+  const u32 c0 = 32 * NSP * L;
+  const bool live = c0 < a.cols;
+  float4 wr[RPW][NQ];
+#pragma unroll
+  for (u32 k = 0; k < RPW; k++) {
+    if (sgi[k] >= a.nseg) continue;
+    const TreeSeg& sg = a.seg[sgi[k]];
+    const u8* rp = sg.W + (u64)row[k] * sg.rb;
+    if (sg.fm == FM_F32) {
+#pragma unroll
+      for (u32 q = 0; q < NQ; q++) wr[k][q] = 64 * q + L < nl4 ? ((const float4*)rp)[64 * q + L] : make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
+#pragma unroll
+      for (u32 q = 0; q < NSP; q++) {
+        float w[32];
+        if (live) span_any(sg.fm, rp, c0 + 32 * q, w);
+        else
+#pragma unroll
+          for (u32 i = 0; i < 32; i++) w[i] = 0.0f;
+#pragma unroll
+        for (u32 g = 0; g < 8; g++) wr[k][8 * q + g] = make_float4(w[4 * g], w[4 * g + 1], w[4 * g + 2], w[4 * g + 3]);
+      }
+    }
+  }
+  // the contiguous layout of x for quantized rows
+#pragma unroll
+  for (u32 q = 0; q < NQ; q++) {
+    const u32 li = 64 * q + L;
+    *(float4*)(xsh + (li / NQ) * LS + 4 * (li % NQ)) = xc[q];
+  }
+  WAVE_SYNC();
+  PHASE(25);
+#pragma unroll
+  for (u32 k = 0; k < RPW; k++) {
+    if (sgi[k] >= a.nseg) break;
+    const TreeSeg& sg = a.seg[sgi[k]];
+    float v;
+    if (sg.fm == FM_F32) {
+      float n[NQ];
+#pragma unroll
+      for (u32 q = 0; q < NQ; q++) n[q] = tree64_asc(leaf4((const float*)&wr[k][q], xc[q]));
+      v = tree_in_lane<NQ>(n);
+    } else {
+      float n[NQ];
+#pragma unroll
+      for (u32 q = 0; q < NQ; q++) n[q] = leaf4((const float*)&wr[k][q], *(const float4*)(xsh + L * LS + 4 * q));
+      v = tree64_asc(live ? tree_in_lane<NQ>(n) : 0.0f);  // a dead lane's leaves are all +0 pads
+    }
+    if (L == 0) sg.out[(u64)t * sg.ostride + row[k]] = sg.bias ? v + sg.bias[row[k]] : v;
+  }
+  PHASE(26);
+}
+template <u32 NSP> constexpr u32 tree_lds() { return 64 * (32 * NSP + 4); }  // floats
+template <u32 NSP>
 __global__ void __launch_bounds__(64) k_tree_rows(TreeArgs a) {
+  __shared__ float xsh[tree_lds<NSP>()];
   BSTAMP(0, 0);
-  tree_body<NSP>(a, blockIdx.x, blockIdx.y, threadIdx.x);
+  tree_body<NSP>(a, blockIdx.x, blockIdx.y, threadIdx.x, xsh);
   BSTAMP(0, 1);
 }
 
@@ -136,9 +182,6 @@ DEV void wave_amax(float& bv, u32& bi) {
   }
 }
 
-// lanes of one wave exchanging words through LDS: a wave's LDS operations complete in issue order,
-// so only the compiler must not move them across this point
-#define WAVE_SYNC() do { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); __builtin_amdgcn_wave_barrier(); } while (0)
 // LDS of topk_body256 (floats): p [1024], sums / tau / count / lane maxima [128], chosen p [64],
 // candidates [256 + 256], the chosen experts [64] (u32)
 #define TOPK_SIDS (1024 + 128 + 64 + 512)
@@ -799,7 +842,7 @@ __global__ void __launch_bounds__(256) k_fused(FusedArgs f) {
     if (it >= total) break;
     if (it < e1) {
       const u32 t = it / f.rpt, sub = it % f.rpt;
-      tree_body<NSP>(f.tr, 4 * sub + w, t, L);
+      tree_body<NSP>(f.tr, 4 * sub + w, t, L, sm + w * tree_lds<NSP>());
       item_done(&c[1]);
     } else if (it < e2) {
       phase_wait(&c[1], f.nR, &c[5], f.spin);
@@ -844,7 +887,8 @@ int launch_tree_rows(const TreeArgs& a, u32 nsp, hipStream_t st) {
   u32 rows = 0;
   for (u32 i = 0; i < a.nseg; i++) rows += a.seg[i].rows;
   if (rows == 0) return 0;
-  dim3 grid((rows + TREE_RPW - 1) / TREE_RPW, a.T);
+  const u32 rpw = tree_rows_per_wave(nsp);
+  dim3 grid((rows + rpw - 1) / rpw, a.T);
   if (nsp == 1) { hipLaunchKernelGGL((k_tree_rows<1>), grid, dim3(64), 0, st, a); return 0; }
   if (nsp == 2) { hipLaunchKernelGGL((k_tree_rows<2>), grid, dim3(64), 0, st, a); return 0; }
   if (nsp == 4) { hipLaunchKernelGGL((k_tree_rows<4>), grid, dim3(64), 0, st, a); return 0; }
@@ -935,10 +979,13 @@ size_t fused_lds(const FusedArgs& f) {
   const size_t dn = ((size_t)f.dn.rw * (f.dn.nk * f.dn.ef / 4 + f.dn.sf / 4) + f.dn.sf + f.dn.rw * nt) * 4;
   const size_t tk = (size_t)TOPK_LDS * 4;  // topk_body256's LDS
   const size_t m = gu > dn ? gu : dn;
-  return m > tk ? m : tk;
+  const size_t tr = (size_t)4 * tree_lds<1>() * 4;  // four waves' tree x (one span a lane)
+  const size_t m2 = m > tk ? m : tk;
+  return m2 > tr ? m2 : tr;
 }
 
 int launch_fused(const FusedArgs& f, u32 fg, u32 fd, u32 fs, u32 nsp, u32 grid, hipStream_t st) {
+  if (nsp != 1) return -1;  // its LDS holds four waves' tree x of one span a lane
   const size_t sm = fused_lds(f);
 #define FU_L(FG, FD, FS) \
   if (fg == FG && fd == FD && fs == FS) { \

@@ -71,6 +71,7 @@ bool fused_supported(uint32_t fg, uint32_t fd, uint32_t fs, uint32_t nsp);
 int launch_tree_rows(const TreeArgs& a, uint32_t nsp, hipStream_t st);
 uint32_t dn_rows(uint32_t nk, uint32_t ef, uint32_t sf);
 int launch_topk(const TopkArgs& a, uint32_t T, hipStream_t st);
+uint32_t tree_rows_per_wave(uint32_t nsp);
 int launch_gu_topk(const GuArgs& a, const TopkArgs& k, uint32_t fg, uint32_t fu, uint32_t nslots, hipStream_t st);
 int launch_gu_exact(const GuArgs& a, uint32_t fg, uint32_t fu, uint32_t nslots, hipStream_t st);
 int launch_dn_exact(const DnArgs& a, uint32_t fd, uint32_t fs, uint32_t T, hipStream_t st);
