@@ -193,25 +193,6 @@ template <> struct Span<FM_Q6_K> {
 // issues the raw loads (so a caller can put a row's loads in flight before it waits on anything
 // else), dec turns them into the same 16 weights span_w gives for those columns.
 
-// 16 bytes from a 2-aligned address, never reading outside p .. p + 15: four aligned dwords from
-// p rounded down, and, when p % 4 == 2, the half dword at p + 14 that the funnel shift by 16 needs.
-// When p % 4 == 0 that fifth word is unused and is read from p + 12 instead (p + 16 can be past the
-// end of the buffer: a Q8_0 block's second half ends 2 bytes before a 4-aligned boundary).
-struct Raw16 { u32 w[5]; };
-DEV Raw16 ld16_a2(const u8* p) {
-  const u32 odd = (u32)(uintptr_t)p & 2u;
-  const u32* a = al4(p);
-  Raw16 r;
-#pragma unroll
-  for (int k = 0; k < 4; k++) r.w[k] = a[k];
-  r.w[4] = (u32)*(const unsigned short*)((const u8*)a + (odd ? 16 : 12));
-  return r;
-}
-DEV void al16(const Raw16& r, u32 sh, u32 o[4]) {
-#pragma unroll
-  for (int k = 0; k < 4; k++) o[k] = __builtin_amdgcn_alignbit(r.w[k + 1], r.w[k], sh);
-}
-
 template <u32 F> struct Half;
 
 template <> struct Half<FM_F32> {
@@ -227,20 +208,25 @@ template <> struct Half<FM_F32> {
   }
 };
 
+// 16 bytes from any address in one load (global loads need no alignment on this target: the
+// compiler itself turns an unaligned 16-byte copy into one global_load_dwordx4)
+DEV uint4 ldu16(const u8* p) {
+  uint4 v;
+  __builtin_memcpy(&v, p, 16);
+  return v;
+}
+
 template <> struct Half<FM_Q8_0> {
-  Raw16 q;
-  u32 d, sh;
+  uint4 q;
+  u32 d;
   MDEV void ld(const u8* row, u32 c0, u32 jh) {
     const u8* B = row + (u64)(c0 >> 5) * 34u;
     d = ld_u16(B);
-    const u8* p = B + 2 + 16 * jh;
-    sh = ((u32)(uintptr_t)p & 2u) * 8u;
-    q = ld16_a2(p);
+    q = ldu16(B + 2 + 16 * jh);
   }
   MDEV void dec(u32, u32, float* w) const {
     const float dv = f16v(d);
-    u32 o[4];
-    al16(q, sh, o);
+    const u32 o[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const u32 v = opq(o[k] ^ 0x80808080u);
@@ -302,32 +288,32 @@ template <> struct Half<FM_Q5_K> {
 };
 
 template <> struct Half<FM_Q6_K> {
-  Raw16 ql, qh;
-  u32 scw, d, sl, sh;
+  uint4 ql, qh;
+  u32 sc, d;
   MDEV void ld(const u8* row, u32 c0, u32 jh) {
     const u8* B = row + (u64)(c0 >> 8) * 210u;
     const u32 r = c0 & 255u, n = r >> 7, quad = (r & 127u) >> 5;
-    const u8* pl = B + 64 * n + 32 * (quad & 1u) + 16 * jh;
-    const u8* ph = B + 128 + 32 * n + 16 * jh;
-    sl = ((u32)(uintptr_t)pl & 2u) * 8u;
-    sh = ((u32)(uintptr_t)ph & 2u) * 8u;
-    ql = ld16_a2(pl);
-    qh = ld16_a2(ph);
-    scw = ld_u16(B + 192 + 8 * n + 2 * quad);
+    ql = ldu16(B + 64 * n + 32 * (quad & 1u) + 16 * jh);
+    qh = ldu16(B + 128 + 32 * n + 16 * jh);
+    sc = (u32)B[192 + (r >> 4) + jh];
     d = ld_u16(B + 208);
   }
-  MDEV void dec(u32 c0, u32 jh, float* w) const {
+  // each byte built as (q ^ 0x20) << 2, which read as a signed byte is 4 (q - 32); (d sc / 4)
+  // (exact: d sc is a normal float or 0) times it is d sc (q - 32), the same exact product, with
+  // the same sign of zero (+0 times d sc)
+  MDEV void dec(u32 c0, u32, float* w) const {
     const u32 r = c0 & 255u, quad = (r & 127u) >> 5;
-    const float ds = f16v(d) * (float)(int)(signed char)((scw >> (8 * jh)) & 255u);
-    const u32 nsh = quad >= 2u ? 4u : 0u, hsh = 2u * quad;
-    u32 l4[4], h4[4];
-    al16(ql, sl, l4);
-    al16(qh, sh, h4);
+    const float ds = f16v(d) * (float)(int)(signed char)sc * 0.25f;
+    const u32 l4[4] = {ql.x, ql.y, ql.z, ql.w}, h4[4] = {qh.x, qh.y, qh.z, qh.w};
+    // the nibble into bits 2..5 of its byte: a rotate by 2 either way (bits that wrap are masked)
+    const u32 rot = quad >= 2u ? 2u : 30u, hs = 6u - 2u * quad;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      const u32 v = opq(((l4[k] >> nsh) & 0x0F0F0F0Fu) | (((h4[k] >> hsh) & 0x03030303u) << 4));
+      const u32 lo = __builtin_amdgcn_alignbit(l4[k], l4[k], rot);
+      const u32 hi = h4[k] << hs;  // bits 2 quad, 2 quad + 1 into 6, 7
+      const u32 v = opq(((lo & 0x3C3C3C3Cu) | (hi & 0xC0C0C0C0u)) ^ 0x80808080u);
 #pragma unroll
-      for (int t = 0; t < 4; t++) w[4 * k + t] = ds * (ubyte(v, t) - 32.0f);
+      for (int t = 0; t < 4; t++) w[4 * k + t] = ds * (float)(int)(signed char)((v >> (8 * t)) & 255u);
     }
   }
 };

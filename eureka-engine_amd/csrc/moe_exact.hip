@@ -28,7 +28,10 @@ __device__ unsigned long long moe_phase_t[64];
 __device__ unsigned long long moe_blk_t[4][4096][2];
 #define BSTAMP(k, i) \
   do { if (threadIdx.x == 0 && blockIdx.x < 4096 && blockIdx.y == 0) moe_blk_t[k][blockIdx.x][i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+// stamp i once v has arrived (the asm takes v as an input, so the wait for it comes first)
+#define PHASE_AFTER(i, v) do { __asm__ volatile("" :: "v"(v)); PHASE(i); } while (0)
 #else
+#define PHASE_AFTER(i, v) do {} while (0)
 #define PHASE(i) do {} while (0)
 #define BSTAMP(k, i) do {} while (0)
 #endif
@@ -701,16 +704,16 @@ __global__ void __launch_bounds__(256) k_gu_topk(GuArgs a, TopkArgs k) {
 
 // down + rank-order combine + gated shared expert + residual, 8 lanes a row. A block takes R
 // outputs of one token and their nt = nk (+ 1 shared) row dots: task k = j R + rl (expert-major, so
-// a wave's groups share one act row and read neighbouring weight rows), tasks gi and gi + 32 of
-// the block's 32 groups (R nt <= 64). The shared down row has the routed rows' format and width
+// a wave's groups share one act row and read neighbouring weight rows), tasks gi + 32 p (p < P) of
+// the block's 32 groups (R nt <= 32 P). The shared down row has the routed rows' format and width
 // (ef = sf = 128 NM).
 //
 // Issue order matters (vmcnt retires in order): ids, then act and the shared gate / up logits into
-// registers, then the weights; act / sa reach LDS while the weights are in flight. The code around
-// the loads is straight-line (per-lane branches make the compiler wait at the joins): tasks past
-// the end load a valid row and are dropped, and staging steps past the end re-copy a word another
-// thread copies too (index min(tid + 256 i, n - 256 + tid), n >= 256).
-template <u32 F, u32 HS, u32 NM>
+// registers, the combine's wt / sgo / x1, then the weights; act / sa reach LDS while the weights
+// are in flight. The code around the loads is straight-line (per-lane branches make the compiler
+// wait at the joins): tasks past the end load a valid row and are dropped, and staging steps past
+// the end re-copy a word another thread copies too (index min(tid + 256 i, n - 256 + tid), n >= 256).
+template <u32 F, u32 HS, u32 NM, u32 P>
 __global__ void __launch_bounds__(256) k_dn_lane(DnArgs a, u32 R) {
   extern __shared__ float sm[];
   BSTAMP(3, 0);
@@ -719,15 +722,17 @@ __global__ void __launch_bounds__(256) k_dn_lane(DnArgs a, u32 R) {
   float* xa = sm;                        // [nk][ef] act of the token's slots
   float* sa = xa + a.nk * a.ef;          // [sf]
   float* part = sa + (HS ? a.sf : 0u);   // [R][nt]
+  float* wts = part + R * nt;            // [nk] wt, then sgo
   const u32 t = blockIdx.y, r0 = blockIdx.x * R;
   const u32 tid = threadIdx.x, gi = tid >> 3, q = tid & 7;
-  u32 kind[2], eid[2];  // kind 0 none, 1 routed, 2 shared
+  u32 kind[P], eid[P];  // kind 0 none, 1 routed, 2 shared
 #pragma unroll
-  for (u32 p = 0; p < 2; p++) {
+  for (u32 p = 0; p < P; p++) {
     const u32 k = gi + 32 * p, j = k / R, r = r0 + k % R;
     kind[p] = (k < ntask && r < a.dm) ? (j < a.nk ? 1u : 2u) : 0u;
     eid[p] = a.ids[(u64)t * a.nk + min(j, a.nk - 1)];
   }
+  PHASE_AFTER(21, eid[0]);
   const float4* act4 = (const float4*)(a.act + (u64)t * a.nk * a.ef);
   const u32 na4 = a.nk * a.ef / 4;  // 256 .. 2048
   // (separate variables, not arrays: the ordering fences below would keep an array in memory)
@@ -740,14 +745,23 @@ __global__ void __launch_bounds__(256) k_dn_lane(DnArgs a, u32 R) {
     const float* g = a.gsu + (u64)t * 2 * a.sf;
     gg0 = g[sc0]; gg1 = g[sc1]; gu0 = g[a.sf + sc0]; gu1 = g[a.sf + sc1];
   }
+  const float wtv = a.wt[(u64)t * a.nk + min(tid, a.nk - 1)];
+  const float sgv = HS ? a.sgo[t] : 0.0f;
+  const float x1v = a.x1 ? a.x1[(u64)t * a.dm + min(r0 + tid, a.dm - 1)] : 0.0f;
+  PHASE_AFTER(22, x1v);
   // the scheduler may not move the weight loads above the staging loads, nor the LDS stores above them
   __asm__ volatile("" ::: "memory");
-  Row8<F, NM> w[2];
+  // a pass whose tasks are all past the end for this wave (the third one, for most waves) loads
+  // nothing: a wave-uniform test
+  const u32 wv0 = 8 * (tid >> 6);  // the wave's first group
+  Row8<F, NM> w[P];
 #pragma unroll
-  for (u32 p = 0; p < 2; p++) {
-    const u32 k = gi + 32 * p, r = min(r0 + k % R, a.dm - 1);
-    const u8* drow = a.D + ((u64)eid[p] * a.dm + r) * a.rbd;
-    w[p].ld(HS && kind[p] == 2 ? a.SD + (u64)r * a.rbs : drow, q);
+  for (u32 p = 0; p < P; p++) {
+    if (p < 2 || wv0 + 32 * p < ntask) {
+      const u32 k = gi + 32 * p, r = min(r0 + k % R, a.dm - 1);
+      const u8* drow = a.D + ((u64)eid[p] * a.dm + r) * a.rbd;
+      w[p].ld(HS && kind[p] == 2 ? a.SD + (u64)r * a.rbs : drow, q);
+    }
   }
   __asm__ volatile("" ::: "memory");
   PHASE(17);
@@ -759,24 +773,24 @@ __global__ void __launch_bounds__(256) k_dn_lane(DnArgs a, u32 R) {
     sa[sc0] = silu_mul(gg0, gu0);
     sa[sc1] = silu_mul(gg1, gu1);
   }
+  if (tid < a.nk) wts[tid] = wtv;
   __syncthreads();
   PHASE(18);
 #pragma unroll
-  for (u32 p = 0; p < 2; p++) {
-    const u32 k = gi + 32 * p, j = k / R, rl = k % R;
-    const float s = w[p].dot(kind[p] == 2 ? sa : xa + min(j, a.nk - 1) * a.ef, q);
-    if (kind[p] && q == 0) part[rl * nt + j] = s;
+  for (u32 p = 0; p < P; p++) {
+    if (p < 2 || wv0 + 32 * p < ntask) {
+      const u32 k = gi + 32 * p, j = k / R, rl = k % R;
+      const float s = w[p].dot(kind[p] == 2 ? sa : xa + min(j, a.nk - 1) * a.ef, q);
+      if (kind[p] && q == 0) part[rl * nt + j] = s;
+    }
   }
   __syncthreads();
   PHASE(19);
   if (tid < R && r0 + tid < a.dm) {
-    const u32 r = r0 + tid;
-    const float* wt = a.wt + (u64)t * a.nk;
     const float* pr = part + tid * nt;
     float mo = 0.0f;
-    for (u32 j = 0; j < a.nk; j++) mo = j == 0 ? pr[0] * wt[0] : mo + pr[j] * wt[j];
-    const float res = a.x1 ? a.x1[(u64)t * a.dm + r] : 0.0f;
-    a.y[(u64)t * a.dm + r] = HS ? (mo + pr[a.nk] * a.sgo[t]) + res : mo + res;
+    for (u32 j = 0; j < a.nk; j++) mo = j == 0 ? pr[0] * wts[0] : mo + pr[j] * wts[j];
+    a.y[(u64)t * a.dm + r0 + tid] = HS ? (mo + pr[a.nk] * sgv) + x1v : mo + x1v;
   }
   PHASE(20);
   BSTAMP(3, 1);
@@ -938,15 +952,25 @@ u32 dn_rows(u32 nk, u32 ef, u32 sf) {
 
 int launch_dn_exact(const DnArgs& a, u32 fd, u32 fs, u32 T, hipStream_t st) {
   const u32 nt = a.nk + (fs ? 1u : 0u);
-  const u32 R = 64 / nt;  // outputs a block: R nt row dots in two passes of 32 groups
   const u32 nm = a.ef / 128;
+  // outputs a block: enough that one token's blocks fit the 256 CUs once (dm / 256), in two or
+  // three passes of the 32 groups; otherwise R nt <= 64 in two passes
+  u32 R = (a.dm + 255) / 256, P = 2;
+  if (R * nt > 64) {
+    if (R * nt <= 96 && nm <= 4) P = 3;
+    else R = 64 / nt;
+  }
   const bool lane = R >= 1 && (fs == 0 || (fs == fd && a.sf == a.ef)) && a.ef % 128 == 0 &&
                     (nm == 2 || nm == 4 || nm == 6 || nm == 8) && a.nk * a.ef >= 1024 && a.nk * a.ef <= 8192;
   if (lane) {
-    const size_t lsm = ((size_t)a.nk * a.ef + (fs ? a.sf : 0) + (size_t)R * nt) * 4;
+    const size_t lsm = ((size_t)a.nk * a.ef + (fs ? a.sf : 0) + (size_t)R * nt + a.nk) * 4;
     const dim3 grid((a.dm + R - 1) / R, T);
 #define DN_N(F, HS, N) \
-  if (nm == N) { hipLaunchKernelGGL((k_dn_lane<F, HS, N>), grid, dim3(256), lsm, st, a, R); return 0; }
+  if (nm == N) { \
+    if (P == 2) hipLaunchKernelGGL((k_dn_lane<F, HS, N, 2>), grid, dim3(256), lsm, st, a, R); \
+    else if constexpr (N <= 4) hipLaunchKernelGGL((k_dn_lane<F, HS, N, 3>), grid, dim3(256), lsm, st, a, R); \
+    return 0; \
+  }
 #define DN_L(F) \
   if (fd == F) { \
     if (fs) { DN_N(F, 1, 2) DN_N(F, 1, 4) DN_N(F, 1, 6) DN_N(F, 1, 8) } \
