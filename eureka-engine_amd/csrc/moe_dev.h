@@ -318,6 +318,71 @@ template <> struct Half<FM_Q6_K> {
   }
 };
 
+// ---- half spans straight to f16 (the grouped-GEMM tier): packed 16-bit arithmetic, two weights an
+// op. A code byte u becomes the half 1024 + u by v_perm with 0x64 as its high byte; subtracting the
+// bias leaves the code exactly. Q8_0: q d rounded once to f16, as rounding the exact f32 product.
+// K-quants: the f32 scale and min products are rounded to f16 first, then one packed FMA a pair
+// (tolerance class, like the f16 activations).
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+DEV h2v as_h2(u32 v) { return __builtin_bit_cast(h2v, v); }
+DEV u32 as_u(h2v v) { return __builtin_bit_cast(u32, v); }
+// bytes 0, 1 (lo) and 2, 3 (hi) of v as 1024 + byte halves
+DEV h2v mag_lo(u32 v) { return as_h2(__builtin_amdgcn_perm(0x64646464u, v, 0x04010400u)); }
+DEV h2v mag_hi(u32 v) { return as_h2(__builtin_amdgcn_perm(0x64646464u, v, 0x04030402u)); }
+DEV h2v h2s(float f) { const _Float16 h = (_Float16)f; return h2v{h, h}; }
+
+template <u32 F> DEV void half_f16(const Half<F>& h, u32 c0, u32 jh, u32* o);
+template <> DEV void half_f16<FM_Q8_0>(const Half<FM_Q8_0>& h, u32, u32, u32* o) {
+  const h2v d = as_h2((h.d & 0xffffu) * 0x10001u), bias = h2s(1152.0f);
+  const u32 q[4] = {h.q.x, h.q.y, h.q.z, h.q.w};
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const u32 u = q[k] ^ 0x80808080u;  // q + 128
+    o[2 * k] = as_u((mag_lo(u) - bias) * d);
+    o[2 * k + 1] = as_u((mag_hi(u) - bias) * d);
+  }
+}
+template <> DEV void half_f16<FM_Q4_K>(const Half<FM_Q4_K>& h, u32 c0, u32, u32* o) {
+  const u32 j = (c0 & 255u) >> 5;
+  u32 sc, mn;
+  k4_scmin(h.h, j, sc, mn);
+  const h2v d1 = h2s(f16v(h.h.x & 0xffffu) * (float)sc), m1 = h2s(-(f16v(h.h.x >> 16) * (float)mn)), bias = h2s(1024.0f);
+  const u32 sh = 4u * (j & 1u);
+  const u32 q[4] = {h.q.x, h.q.y, h.q.z, h.q.w};
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const u32 v = (q[k] >> sh) & 0x0F0F0F0Fu;
+    o[2 * k] = as_u(__builtin_elementwise_fma(mag_lo(v) - bias, d1, m1));
+    o[2 * k + 1] = as_u(__builtin_elementwise_fma(mag_hi(v) - bias, d1, m1));
+  }
+}
+template <> DEV void half_f16<FM_Q5_K>(const Half<FM_Q5_K>& h, u32 c0, u32, u32* o) {
+  const u32 j = (c0 & 255u) >> 5;
+  u32 sc, mn;
+  k4_scmin(h.h, j, sc, mn);
+  const h2v d1 = h2s(f16v(h.h.x & 0xffffu) * (float)sc), m1 = h2s(-(f16v(h.h.x >> 16) * (float)mn)), bias = h2s(1024.0f);
+  const u32 sh = 4u * (j & 1u);
+  const u32 q[4] = {h.q.x, h.q.y, h.q.z, h.q.w}, hh[4] = {h.qh.x, h.qh.y, h.qh.z, h.qh.w};
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const u32 v = ((q[k] >> sh) & 0x0F0F0F0Fu) | (((hh[k] >> j) & 0x01010101u) << 4);
+    o[2 * k] = as_u(__builtin_elementwise_fma(mag_lo(v) - bias, d1, m1));
+    o[2 * k + 1] = as_u(__builtin_elementwise_fma(mag_hi(v) - bias, d1, m1));
+  }
+}
+template <> DEV void half_f16<FM_Q6_K>(const Half<FM_Q6_K>& h, u32 c0, u32, u32* o) {
+  const u32 r = c0 & 255u, quad = (r & 127u) >> 5;
+  const h2v ds = h2s(f16v(h.d) * (float)(int)(signed char)h.sc), bias = h2s(1056.0f);  // 1024 + 32
+  const u32 nsh = quad >= 2u ? 4u : 0u, hsh = 2u * quad;
+  const u32 l4[4] = {h.ql.x, h.ql.y, h.ql.z, h.ql.w}, h4[4] = {h.qh.x, h.qh.y, h.qh.z, h.qh.w};
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const u32 v = ((l4[k] >> nsh) & 0x0F0F0F0Fu) | (((h4[k] >> hsh) & 0x03030303u) << 4);
+    o[2 * k] = as_u((mag_lo(v) - bias) * ds);
+    o[2 * k + 1] = as_u((mag_hi(v) - bias) * ds);
+  }
+}
+
 // ---- cross-lane pair sums at ALU latency (DPP and the gfx950 permlane swaps; ds_bpermute, which
 // __shfl_xor uses, costs about 60 ns a step). xaddM(v) = v + v[lane ^ M]; IEEE addition commutes, so
 // the value is the exact pair sum. Lanes where it holds: M = 1, 2, 8, 16, 32 every lane; M = 4 the

@@ -151,6 +151,160 @@ __global__ void __launch_bounds__(256) k_moe_gemm(GemmArgs g) {
     }
 }
 
+// ---- the pipelined grouped GEMM. Block tile: BM = 128 slots x 128 B rows (mode 0: 64 gate + 64 up
+// features, mode 1: 128 features), K in steps of 64, four waves of 64 x 64 (2 x 2 MFMA 32x32x16
+// tiles; in mode 0 one wave's gate and up tiles cover the same 32 features, so the SwiGLU epilogue
+// pairs them in registers). LDS holds two stages of A and B (f16, rows padded to 72 halves): while
+// the MFMAs run on one stage, the next tile's A rows and raw weight half-spans are in flight into
+// registers; after the MFMAs they are dequantized into the other stage. One barrier a k-tile.
+#define G2_BK 64
+#define G2_LD 72
+#define G2_STAGE (2 * GM_BM * G2_LD)  // halves: A [128][72] then B [128][72]
+
+// XCD-aware order: the hardware deals block b to XCD b % 8, so block b takes m-tile
+// 8 ((b / 8) / NT) + b % 8 and feature tile (b / 8) % NT: an m-tile's NT feature tiles all run on
+// one XCD and read its activation rows from that XCD's L2 (1-D grid, 8 NT ceil(tiles / 8) blocks)
+template <u32 F, u32 MODE>
+__global__ void __launch_bounds__(256, 2) k_moe_gemm2(GemmArgs g, u32 NT) {
+  extern __shared__ _Float16 lds[];
+  const u32 bi = blockIdx.x >> 3, tile = 8 * (bi / NT) + (blockIdx.x & 7), ntile = bi % NT;
+  u32 e, m0, base, M;
+  if (g.tiles) {
+    if (tile >= *g.ntiles) return;
+    const u32 tv = g.tiles[tile];
+    e = tv >> 16;
+    m0 = (tv & 0xffffu) * GM_BM;
+    base = g.off[e];
+    M = g.off[e + 1] - base;
+  } else {
+    e = 0;
+    m0 = tile * GM_BM;
+    base = 0;
+    M = g.M;
+    if (m0 >= M) return;
+  }
+  constexpr u32 NF = MODE == 0 ? 64u : 128u;  // output features a block
+  const u32 n0 = ntile * NF, tid = threadIdx.x, w = tid >> 6, l = tid & 63, wm = w >> 1, wn = w & 1;
+  // A: 128 rows x 64 halves a k-tile, 16-byte chunks c = tid + 256 i (i < 4): row c / 8, chunk c % 8
+  const _Float16* asrc[4];
+  bool aok[4];
+#pragma unroll
+  for (u32 i = 0; i < 4; i++) {
+    const u32 c = tid + 256 * i, r = c >> 3;
+    aok[i] = m0 + r < M;
+    const u64 s = base + m0 + (aok[i] ? r : 0u);
+    const u64 src = MODE == 0 ? (g.xmap ? (u64)g.xmap[s] : s) : s;
+    asrc[i] = g.A + src * g.K + 8 * (c & 7);
+  }
+  // B: 128 rows x 64 columns a k-tile; thread: row tid / 2, span tid % 2 (two half-spans)
+  const u32 br = tid >> 1, bs = tid & 1;
+  const u8* brow;
+  if (MODE == 0) brow = (br < 64 ? g.W0 + (u64)(n0 + br) * g.rb : g.W1 + (u64)(n0 + br - 64) * g.rb) + (u64)e * g.es;
+  else brow = g.W0 + (u64)e * g.es + (u64)(n0 + br) * g.rb;
+
+  // three register slots keep k-tiles t + 2 .. t + 4 in flight while tile t is multiplied (slot of
+  // tile u: u % 3); compile-time slot choice keeps them in registers
+  struct Slot {
+    uint4 a[4];
+    Half<F> h[2];
+  };
+  Slot s0, s1, s2;
+  const u32 nk = g.K / G2_BK;
+  auto load = [&](Slot& s, u32 t) {
+    if (t >= nk) return;
+    const u32 k0 = t * G2_BK;
+#pragma unroll
+    for (u32 i = 0; i < 4; i++) s.a[i] = aok[i] ? *(const uint4*)(asrc[i] + k0) : make_uint4(0, 0, 0, 0);
+    s.h[0].ld(brow, k0 + 32 * bs, 0);
+    s.h[1].ld(brow, k0 + 32 * bs, 1);
+  };
+  auto store = [&](const Slot& s, u32 t) {
+    _Float16* As = lds + (t & 1) * G2_STAGE;
+    _Float16* Bs = As + GM_BM * G2_LD;
+    const u32 k0 = t * G2_BK;
+#pragma unroll
+    for (u32 i = 0; i < 4; i++) {
+      const u32 c = tid + 256 * i;
+      *(uint4*)(As + (c >> 3) * G2_LD + 8 * (c & 7)) = s.a[i];
+    }
+#pragma unroll
+    for (u32 j = 0; j < 2; j++) {
+      u32 o[8];
+      half_f16<F>(s.h[j], k0 + 32 * bs, j, o);
+      _Float16* d = Bs + br * G2_LD + 32 * bs + 16 * j;
+      *(uint4*)d = make_uint4(o[0], o[1], o[2], o[3]);
+      *(uint4*)(d + 8) = make_uint4(o[4], o[5], o[6], o[7]);
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (u32 a = 0; a < 2; a++)
+#pragma unroll
+    for (u32 b = 0; b < 2; b++)
+#pragma unroll
+      for (u32 i = 0; i < 16; i++) acc[a][b][i] = 0.0f;
+  // B rows of this wave's two 32-column tiles
+  const u32 bro0 = MODE == 0 ? 32 * wn : 64 * wn, bro1 = MODE == 0 ? 64 + 32 * wn : 64 * wn + 32;
+  auto mma = [&](u32 t) {
+    const _Float16* As = lds + (t & 1) * G2_STAGE;
+    const _Float16* Bs = As + GM_BM * G2_LD;
+#pragma unroll
+    for (u32 ks = 0; ks < G2_BK / 16; ks++) {
+      const u32 ko = 16 * ks + 8 * (l >> 5);
+      const h8 a0 = *(const h8*)(As + (64 * wm + (l & 31)) * G2_LD + ko);
+      const h8 a1 = *(const h8*)(As + (64 * wm + 32 + (l & 31)) * G2_LD + ko);
+      const h8 b0 = *(const h8*)(Bs + (bro0 + (l & 31)) * G2_LD + ko);
+      const h8 b1 = *(const h8*)(Bs + (bro1 + (l & 31)) * G2_LD + ko);
+      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, acc[0][0], 0, 0, 0);
+      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b1, acc[0][1], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b0, acc[1][0], 0, 0, 0);
+      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, acc[1][1], 0, 0, 0);
+    }
+  };
+  // iteration t: multiply tile t, store tile t + 1 (its slot) into the other stage, refill that
+  // slot with tile t + 4, one barrier
+  auto step = [&](Slot& s, u32 t) {
+    mma(t);
+    if (t + 1 < nk) {
+      store(s, t + 1);
+      load(s, t + 4);
+    }
+    __syncthreads();
+  };
+  load(s0, 0);
+  load(s1, 1);
+  load(s2, 2);
+  store(s0, 0);
+  load(s0, 3);
+  __syncthreads();
+  u32 t = 0;
+  for (; t + 3 <= nk; t += 3) {
+    step(s1, t);
+    step(s2, t + 1);
+    step(s0, t + 2);
+  }
+  if (t < nk) step(s1, t);
+  if (t + 1 < nk) step(s2, t + 1);
+  // epilogue: acc[a][b][i] is row 64 wm + 32 a + 8 (i / 4) + 4 (l / 32) + i % 4 of the tile,
+  // column l % 32 of B tile b
+#pragma unroll
+  for (u32 a = 0; a < 2; a++)
+#pragma unroll
+    for (u32 i = 0; i < 16; i++) {
+      const u32 row = 64 * wm + 32 * a + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
+      if (m0 + row >= M) continue;
+      const u64 s = base + m0 + row;
+      if (MODE == 0) {
+        const float gv = acc[a][0][i], uv = acc[a][1][i];
+        ((_Float16*)g.out)[s * g.N + n0 + 32 * wn + (l & 31)] = (_Float16)(gv / (1.0f + __expf(-gv)) * uv);
+      } else {
+#pragma unroll
+        for (u32 b = 0; b < 2; b++) ((float*)g.out)[s * g.N + n0 + 64 * wn + 32 * b + (l & 31)] = acc[a][b][i];
+      }
+    }
+}
+
 // y[t][r] = (sum_j, rank order, wt[t][j] out[inv[t nk + j]][r]) + sgo[t] shd[t][r] + x1[t][r]
 __global__ void __launch_bounds__(256) k_combine(const float* __restrict__ out, const u32* __restrict__ inv,
                                                  const float* __restrict__ wt, u32 nk, const float* __restrict__ shd,
@@ -182,7 +336,30 @@ template <u32 F, u32 MODE> static void gemm_go(const GemmArgs& g, dim3 grid, siz
   hipLaunchKernelGGL((k_moe_gemm<F, MODE>), grid, dim3(256), sm, st, g);
 }
 
+template <u32 F, u32 MODE> static void gemm2_go(const GemmArgs& g, dim3 grid, size_t sm, hipStream_t st) {
+  static bool set = false;
+  if (!set) {
+    (void)hipFuncSetAttribute((const void*)k_moe_gemm2<F, MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
+    set = true;
+  }
+  hipLaunchKernelGGL((k_moe_gemm2<F, MODE>), grid, dim3(256), sm, st, g, g.N / (MODE == 0 ? 64u : 128u));
+}
+
 int launch_moe_gemm(const GemmArgs& g, u32 fm, u32 mode, u32 grid_y, hipStream_t st) {
+  const u32 nf = mode == 0 ? 64u : 128u;
+  if (g.K % G2_BK == 0 && g.N % nf == 0 && fm != FM_F32) {
+    const dim3 grid(8 * (g.N / nf) * ((grid_y + 7) / 8));
+    const size_t sm = (size_t)2 * G2_STAGE * 2;
+#define G2_L(F) \
+  if (fm == F) { \
+    if (mode == 0) gemm2_go<F, 0>(g, grid, sm, st); \
+    else gemm2_go<F, 1>(g, grid, sm, st); \
+    return 0; \
+  }
+    G2_L(FM_Q8_0) G2_L(FM_Q4_K) G2_L(FM_Q6_K) G2_L(FM_Q5_K)
+#undef G2_L
+    return -1;
+  }
   if (g.K % GM_BK || g.N % GM_BN) return -1;
   const dim3 grid(g.N / GM_BN, grid_y);
   const size_t sm = gemm_lds(mode);
