@@ -25,6 +25,16 @@ import eureka_moe as em  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 
 
+def measured_traffic(workload, stage, applies=True):
+    """HBM bytes per launch of a stage's kernel, as rocprofv3 FETCH_SIZE / WRITE_SIZE passes measured it
+    (calibrated against a copy of known size): profiles/traffic.json. None when not measured."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            return json.load(f)[workload][stage] if applies else None
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def stage_bytes(shape, T=1):
     """algorithmic HBM bytes per launch of each stage for T = 1 decode (every selected expert distinct)."""
     s = shape
@@ -41,7 +51,7 @@ def stage_bytes(shape, T=1):
 MFMA_F16_PEAK_TFS = 2500.0
 
 
-def prefill(dev, shape, T, layers, steps, warmup):
+def prefill(dev, shape, T, layers, steps, warmup, name=""):
     """T-token chunks through `layers` resident layers on the f16 MFMA tier: tokens/s, and the gate/up
     GEMM's MFMA rate (algorithmic flops 2 T nk dm ef x 2 per launch over its HIP-event time)."""
     Ls = [em.Layer(dev, shape, seed=1, layer=100 + i) for i in range(layers)]
@@ -76,6 +86,7 @@ def prefill(dev, shape, T, layers, steps, warmup):
             "layers": layers, "stages_us": {k: round(v[0], 2) for k, v in st.items()},
             "roofline": {"bound": "mfma", "kernel": "gate_up GEMM (f16 MFMA)", "achieved": round(ach, 1),
                          "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFS, 4),
+                         "traffic": measured_traffic(f"{name}_prefill_{T}", "gate_up"), "kernel_us": round(gu_us, 2),
                          "weight_gbs": round(wbytes / (gu_us * 1e-6) / 1e9, 1)}}
 
 
@@ -142,11 +153,22 @@ def main():
     ap.add_argument("--no-prefill", dest="prefill", action="store_false", help="skip the prefill leg")
     ap.add_argument("--prefill-config", default="c1")
     ap.add_argument("--prefill-T", type=int, default=2048)
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only run three 256 MiB device-to-device copies (the PMC byte-counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the MoE path is not sharded across GPUs); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calib:
+        dev = em.Device(0)
+        n = 256 << 20
+        src, dst = dev.alloc(n), dev.alloc(n)
+        for _ in range(3):
+            dev.check(dev.lib.llb_hip_copy(dst, src, n))
+        dev.sync()
+        print(json.dumps({"copy_calib_bytes": 3 * n}), flush=True)
+        return
 
     shape = em.SHAPES[args.config]
     tier = em.EXACT if args.tier == "exact" else em.Q8
@@ -219,8 +241,9 @@ def main():
         "layer_frac_hbm": round(layer_bytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "stages_us": {k: round(v[0], 3) for k, v in stages.items()},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": sbytes[dom]},
+                     "frac": round(ach / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(f"{args.config}_decode", dom, args.tier == "exact"),
+                     "bytes_per_launch": sbytes[dom], "kernel_us": round(dom_us, 3)},
     }
     if args.prefill:
         b3 = {}
@@ -231,8 +254,11 @@ def main():
             L.free()
         layers.clear()
         pshape = em.SHAPES[args.prefill_config]
-        out["prefill"] = prefill(dev, pshape, args.prefill_T, 4, max(2, args.steps // 4), 1)
+        out["prefill"] = prefill(dev, pshape, args.prefill_T, 4, max(2, args.steps // 4), 1, args.prefill_config)
         out["prefill"]["config"] = f"{args.prefill_config} layer, {args.prefill_T}-token chunk, f16 MFMA tier"
+        # the same layer shape with Q4_K gate / up and Q6_K down weight tiles
+        out["prefill_k_quants"] = prefill(dev, em.SHAPES["c1k"], args.prefill_T, 4, max(2, args.steps // 4), 1, "c1k")
+        out["prefill_k_quants"]["config"] = f"c1k layer (Q4_K gate/up, Q6_K down), {args.prefill_T}-token chunk, f16 MFMA tier"
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(shape)
     print(json.dumps(out), flush=True)

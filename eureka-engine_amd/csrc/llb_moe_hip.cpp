@@ -51,19 +51,37 @@ struct StageEv {
   long cnt;
 };
 static StageEv g_ev[ST_NSTAGE];
+// one-kernel stages are armed here and timed by the GPU around that kernel (LAUNCH_K);
+// ST_Q8X (several kernels) records stream events around them
+static int g_armed = -1, g_fired = -1;
 void stage_begin(int s) {
   if (!g_timing || g_capturing) return;
   StageEv& e = g_ev[s];
   if (e.n >= 64) return;
   if (!e.a[e.n]) { (void)hipEventCreate(&e.a[e.n]); (void)hipEventCreate(&e.b[e.n]); }
-  (void)hipEventRecord(e.a[e.n], g_stream);
+  if (s == ST_Q8X) (void)hipEventRecord(e.a[e.n], g_stream);
+  else g_armed = s;
+}
+bool stage_armed(hipEvent_t* a, hipEvent_t* b) {
+  if (g_armed < 0) return false;
+  StageEv& e = g_ev[g_armed];
+  *a = e.a[e.n];
+  *b = e.b[e.n];
+  g_fired = g_armed;
+  g_armed = -1;
+  return true;
 }
 void stage_end(int s) {
   if (!g_timing || g_capturing) return;
   StageEv& e = g_ev[s];
   if (e.n >= 64) return;
-  (void)hipEventRecord(e.b[e.n], g_stream);
-  e.n++;
+  if (s == ST_Q8X) {
+    (void)hipEventRecord(e.b[e.n], g_stream);
+    e.n++;
+  } else if (g_fired == s) {
+    e.n++;
+  }
+  g_armed = g_fired = -1;
 }
 static void stage_collect() {
   for (int s = 0; s < ST_NSTAGE; s++) {
@@ -436,9 +454,10 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
     return fused_forward(L, T, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt), sc, s);
   if (tier == LLB_MOE_F16)
     return gemm_forward(L, T, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt), sc, s);
-  // the exact tier routes inside its gate / up launch (one launch fewer a layer)
+  // one token: the exact tier routes inside its gate / up launch (one launch fewer a layer; every
+  // block recomputes the token's routing, which only pays off for a single token)
   TopkArgs tk{};
-  const bool fuse_topk = tier == LLB_MOE_EXACT && fg == fu;
+  const bool fuse_topk = tier == LLB_MOE_EXACT && fg == fu && T == 1;
   if ((rc = route(L, T, dp<float>(h2), dp<uint32_t>(ids), dp<float>(wt), sc, s, true, fuse_topk ? &tk : nullptr)))
     return rc;
   const uint64_t rbg = row_bytes(fg, L->dm), rbu = row_bytes(fu, L->dm);

@@ -903,14 +903,14 @@ int launch_tree_rows(const TreeArgs& a, u32 nsp, hipStream_t st) {
   if (rows == 0) return 0;
   const u32 rpw = tree_rows_per_wave(nsp);
   dim3 grid((rows + rpw - 1) / rpw, a.T);
-  if (nsp == 1) { hipLaunchKernelGGL((k_tree_rows<1>), grid, dim3(64), 0, st, a); return 0; }
-  if (nsp == 2) { hipLaunchKernelGGL((k_tree_rows<2>), grid, dim3(64), 0, st, a); return 0; }
-  if (nsp == 4) { hipLaunchKernelGGL((k_tree_rows<4>), grid, dim3(64), 0, st, a); return 0; }
+  if (nsp == 1) { LAUNCH_K((k_tree_rows<1>), grid, dim3(64), 0, st, a); return 0; }
+  if (nsp == 2) { LAUNCH_K((k_tree_rows<2>), grid, dim3(64), 0, st, a); return 0; }
+  if (nsp == 4) { LAUNCH_K((k_tree_rows<4>), grid, dim3(64), 0, st, a); return 0; }
   return -1;
 }
 
 int launch_topk(const TopkArgs& a, u32 T, hipStream_t st) {
-  hipLaunchKernelGGL(k_topk, dim3(T), dim3(256), 0, st, a);
+  LAUNCH_K(k_topk, dim3(T), dim3(256), 0, st, a);
   return 0;
 }
 
@@ -920,8 +920,8 @@ int launch_gu_exact(const GuArgs& a, u32 fg, u32 fu, u32 nslots, hipStream_t st)
   const size_t sm = (size_t)a.dm * 4;
 #define GU_L(F) \
   if (fg == F) { \
-    if (a.dm == 2048) hipLaunchKernelGGL((k_gu_lane<F, 16>), grid, dim3(256), sm, st, a); \
-    else hipLaunchKernelGGL((k_gu_lane<F, 0>), grid, dim3(256), sm, st, a); \
+    if (a.dm == 2048) LAUNCH_K((k_gu_lane<F, 16>), grid, dim3(256), sm, st, a); \
+    else LAUNCH_K((k_gu_lane<F, 0>), grid, dim3(256), sm, st, a); \
     return 0; \
   }
   FM_CASES(GU_L)
@@ -935,8 +935,8 @@ int launch_gu_topk(const GuArgs& a, const TopkArgs& k, u32 fg, u32 fu, u32 nslot
   const size_t sm = ((size_t)TOPK_LDS + a.dm) * 4;
 #define GU_L(F) \
   if (fg == F) { \
-    if (a.dm == 2048) hipLaunchKernelGGL((k_gu_topk<F, 16>), grid, dim3(256), sm, st, a, k); \
-    else hipLaunchKernelGGL((k_gu_topk<F, 0>), grid, dim3(256), sm, st, a, k); \
+    if (a.dm == 2048) LAUNCH_K((k_gu_topk<F, 16>), grid, dim3(256), sm, st, a, k); \
+    else LAUNCH_K((k_gu_topk<F, 0>), grid, dim3(256), sm, st, a, k); \
     return 0; \
   }
   FM_CASES(GU_L)
@@ -967,8 +967,8 @@ int launch_dn_exact(const DnArgs& a, u32 fd, u32 fs, u32 T, hipStream_t st) {
     const dim3 grid((a.dm + R - 1) / R, T);
 #define DN_N(F, HS, N) \
   if (nm == N) { \
-    if (P == 2) hipLaunchKernelGGL((k_dn_lane<F, HS, N, 2>), grid, dim3(256), lsm, st, a, R); \
-    else if constexpr (N <= 4) hipLaunchKernelGGL((k_dn_lane<F, HS, N, 3>), grid, dim3(256), lsm, st, a, R); \
+    if (P == 2) LAUNCH_K((k_dn_lane<F, HS, N, 2>), grid, dim3(256), lsm, st, a, R); \
+    else if constexpr (N <= 4) LAUNCH_K((k_dn_lane<F, HS, N, 3>), grid, dim3(256), lsm, st, a, R); \
     return 0; \
   }
 #define DN_L(F) \
@@ -984,7 +984,7 @@ int launch_dn_exact(const DnArgs& a, u32 fd, u32 fs, u32 T, hipStream_t st) {
   dim3 grid((a.dm + a.rw - 1) / a.rw, T);
   const size_t sm = ((size_t)a.rw * (a.nk * a.ef / 4 + (fs ? a.sf / 4 : 0)) + (fs ? a.sf : 0) + a.rw * nt) * 4;
 #define DN_L(FD, FS) \
-  if (fd == FD && fs == FS) { hipLaunchKernelGGL((k_dn_exact<FD, FS>), grid, dim3(256), sm, st, a); return 0; }
+  if (fd == FD && fs == FS) { LAUNCH_K((k_dn_exact<FD, FS>), grid, dim3(256), sm, st, a); return 0; }
 #define DN_FS(FD) DN_L(FD, 0u) DN_L(FD, FM_Q4_K) DN_L(FD, FM_Q6_K) DN_L(FD, FM_Q5_K)
   FM_CASES(DN_FS)
 #undef DN_FS
@@ -1013,8 +1013,8 @@ int launch_fused(const FusedArgs& f, u32 fg, u32 fd, u32 fs, u32 nsp, u32 grid, 
   const size_t sm = fused_lds(f);
 #define FU_L(FG, FD, FS) \
   if (fg == FG && fd == FD && fs == FS) { \
-    if (nsp == 1) { hipLaunchKernelGGL((k_fused<FG, FD, FS, 1>), dim3(grid), dim3(256), sm, st, f); return 0; } \
-    if (nsp == 2) { hipLaunchKernelGGL((k_fused<FG, FD, FS, 2>), dim3(grid), dim3(256), sm, st, f); return 0; } \
+    if (nsp == 1) { LAUNCH_K((k_fused<FG, FD, FS, 1>), dim3(grid), dim3(256), sm, st, f); return 0; } \
+    if (nsp == 2) { LAUNCH_K((k_fused<FG, FD, FS, 2>), dim3(grid), dim3(256), sm, st, f); return 0; } \
   }
   FUSED_CASES(FU_L)
 #undef FU_L
@@ -1031,7 +1031,7 @@ int launch_dequant(u32 fm, const u8* W, u64 rb, u32 rows, u32 cols, float* out, 
   const u64 n = (u64)rows * (cols / 32);
   dim3 grid((u32)((n + 255) / 256));
 #define DQ_L(F) \
-  if (fm == F) { hipLaunchKernelGGL((k_dequant<F>), grid, dim3(256), 0, st, W, rb, rows, cols, out); return 0; }
+  if (fm == F) { LAUNCH_K((k_dequant<F>), grid, dim3(256), 0, st, W, rb, rows, cols, out); return 0; }
   FM_CASES(DQ_L) DQ_L(FM_F32)
 #undef DQ_L
   return -1;

@@ -333,7 +333,7 @@ template <u32 F, u32 MODE> static void gemm_go(const GemmArgs& g, dim3 grid, siz
     (void)hipFuncSetAttribute((const void*)k_moe_gemm<F, MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
     set = true;
   }
-  hipLaunchKernelGGL((k_moe_gemm<F, MODE>), grid, dim3(256), sm, st, g);
+  LAUNCH_K((k_moe_gemm<F, MODE>), grid, dim3(256), sm, st, g);
 }
 
 template <u32 F, u32 MODE> static void gemm2_go(const GemmArgs& g, dim3 grid, size_t sm, hipStream_t st) {
@@ -342,7 +342,7 @@ template <u32 F, u32 MODE> static void gemm2_go(const GemmArgs& g, dim3 grid, si
     (void)hipFuncSetAttribute((const void*)k_moe_gemm2<F, MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
     set = true;
   }
-  hipLaunchKernelGGL((k_moe_gemm2<F, MODE>), grid, dim3(256), sm, st, g, g.N / (MODE == 0 ? 64u : 128u));
+  LAUNCH_K((k_moe_gemm2<F, MODE>), grid, dim3(256), sm, st, g, g.N / (MODE == 0 ? 64u : 128u));
 }
 
 int launch_moe_gemm(const GemmArgs& g, u32 fm, u32 mode, u32 grid_y, hipStream_t st) {

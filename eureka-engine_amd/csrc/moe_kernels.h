@@ -1,9 +1,21 @@
 // moe_kernels.h -- kernel argument blocks and launchers shared by the HIP sources and the C-ABI.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 
 enum { ST_ROUTE, ST_TOPK, ST_GU, ST_DN, ST_Q8X, ST_NSTAGE };
+// Stage timing. A stage other than ST_Q8X is one kernel: stage_begin arms it, and the next launch
+// made through LAUNCH_K takes the armed event pair, which hipExtLaunchKernelGGL has the GPU record
+// around that kernel alone (no launch gap in the figure). ST_Q8X (several kernels) records plain
+// stream events around them.
+bool stage_armed(hipEvent_t* a, hipEvent_t* b);
+#define LAUNCH_K(K, G, B, S, ST, ...)                                                   \
+  do {                                                                                   \
+    hipEvent_t ea_, eb_;                                                                 \
+    if (stage_armed(&ea_, &eb_)) hipExtLaunchKernelGGL(K, G, B, S, ST, ea_, eb_, 0, __VA_ARGS__); \
+    else hipLaunchKernelGGL(K, G, B, S, ST, __VA_ARGS__);                                \
+  } while (0)
 void stage_begin(int s);
 void stage_end(int s);
 

@@ -294,12 +294,12 @@ int moe_q8_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const fl
   stage_end(ST_Q8X);
   const uint32_t tasks = (uint32_t)(n * L->ef + (size_t)T * L->sf) / 16;
   stage_begin(ST_GU);
-  hipLaunchKernelGGL(k_gu_q8, dim3(tasks), dim3(128), 0, st, a, (u32)n);
+  LAUNCH_K(k_gu_q8, dim3(tasks), dim3(128), 0, st, a, (u32)n);
   stage_end(ST_GU);
   launch_q8_1(a.act, (uint32_t)(n * L->ef), a.aq, a.ad, st);
   if (L->sf) launch_q8_1(a.sa, T * L->sf, a.sq, a.sd2, st);
   stage_begin(ST_DN);
-  hipLaunchKernelGGL(k_dn_q8, dim3((L->dm + a.rw - 1) / a.rw, T), dim3(256), 0, st, a);
+  LAUNCH_K(k_dn_q8, dim3((L->dm + a.rw - 1) / a.rw, T), dim3(256), 0, st, a);
   stage_end(ST_DN);
   return 0;
 }
