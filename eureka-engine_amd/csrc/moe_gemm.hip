@@ -10,8 +10,6 @@
 // then y[t] = (sum over ranks j, in order, wt[t][j] out[inv[t nk + j]]) + sgo[t] shd[t] + x1[t].
 // The shared expert is the same two GEMMs over all T tokens (one "expert", identity map).
 //
-// Block tile: BM = 128 slots x BN = 64 outputs (x2 matrices for gate / up), K in steps of BK = 128.
-// Wave w computes rows 32 w .. 32 w + 31 of the tile, both 32-column halves, each matrix.
 #include "../../include/llb_moe_hip.h"
 #include "moe_dev.h"
 #include "moe_kernels.h"
@@ -19,10 +17,7 @@
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-#define GM_BM 128
-#define GM_BN 64
-#define GM_BK 128
-#define GM_LD (GM_BK + 8)  // halves per LDS row: the pad spreads a wave's 16-byte row reads over banks
+#define GM_BM 256  // slots a tile (an expert's slots split into tiles of this many)
 
 // f32 rows -> f16 rows (the activations' one conversion)
 __global__ void __launch_bounds__(256) k_to_f16(const float* __restrict__ x, _Float16* __restrict__ y, u64 n) {
@@ -59,113 +54,23 @@ __global__ void __launch_bounds__(1024) k_tiles(const u32* __restrict__ off, u32
   if (t == 1023) *ntiles = part[1023];
 }
 
-// MODE 0: gate / up with the SwiGLU epilogue, A = f16 rows of x gathered through xmap, out f16 act.
-// MODE 1: down, A = f16 act rows (slot order), out f32.
-template <u32 F, u32 MODE>
-__global__ void __launch_bounds__(256) k_moe_gemm(GemmArgs g) {
-  extern __shared__ _Float16 lds[];
-  constexpr u32 NB = MODE == 0 ? 2u : 1u;
-  _Float16* As = lds;                      // [BM][LD]
-  _Float16* Bs = lds + GM_BM * GM_LD;      // [NB][BN][LD]
-  u32 e, m0, base, M;
-  if (g.tiles) {
-    if (blockIdx.y >= *g.ntiles) return;
-    const u32 tv = g.tiles[blockIdx.y];
-    e = tv >> 16;
-    m0 = (tv & 0xffffu) * GM_BM;
-    base = g.off[e];
-    M = g.off[e + 1] - base;
-  } else {
-    e = 0;
-    m0 = blockIdx.y * GM_BM;
-    base = 0;
-    M = g.M;
-    if (m0 >= M) return;
-  }
-  const u32 n0 = blockIdx.x * GM_BN, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-  const u8* W0 = g.W0 + (u64)e * g.es;
-  const u8* W1 = MODE == 0 ? g.W1 + (u64)e * g.es : nullptr;
-  f32x16 acc[NB][2];
-#pragma unroll
-  for (u32 b = 0; b < NB; b++)
-#pragma unroll
-    for (u32 h = 0; h < 2; h++)
-#pragma unroll
-      for (u32 i = 0; i < 16; i++) acc[b][h][i] = 0.0f;
-
-  for (u32 k0 = 0; k0 < g.K; k0 += GM_BK) {
-    // A: BM rows x BK halves, 16-byte chunks (8 halves): 2048 chunks, 8 a thread
-#pragma unroll
-    for (u32 q = 0; q < GM_BM * GM_BK / 8 / 256; q++) {
-      const u32 c = tid + 256 * q, r = c / (GM_BK / 8), kc = c % (GM_BK / 8);
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (m0 + r < M) {
-        const u64 s = base + m0 + r;
-        const u64 src = MODE == 0 ? (g.xmap ? (u64)g.xmap[s] : s) : s;
-        v = *(const uint4*)(g.A + src * g.K + k0 + 8 * kc);
-      }
-      *(uint4*)(As + r * GM_LD + 8 * kc) = v;
-    }
-    // B: NB x BN rows x BK columns of weights, a 32-column span a task
-    for (u32 it = tid; it < NB * GM_BN * (GM_BK / 32); it += 256) {
-      const u32 b = it / (GM_BN * (GM_BK / 32)), rr = (it / (GM_BK / 32)) % GM_BN, sp = it % (GM_BK / 32);
-      float wv[32];
-      Span<F>::w((b == 0 ? W0 : W1) + (u64)(n0 + rr) * g.rb, k0 + 32 * sp, wv);
-      _Float16* dst = Bs + (b * GM_BN + rr) * GM_LD + 32 * sp;
-#pragma unroll
-      for (u32 q = 0; q < 4; q++) {
-        h8 hv;
-#pragma unroll
-        for (u32 i = 0; i < 8; i++) hv[i] = (_Float16)wv[8 * q + i];
-        *(h8*)(dst + 8 * q) = hv;
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (u32 ks = 0; ks < GM_BK / 16; ks++) {
-      const h8 a = *(const h8*)(As + (32 * w + (l & 31)) * GM_LD + 16 * ks + 8 * (l >> 5));
-#pragma unroll
-      for (u32 b = 0; b < NB; b++)
-#pragma unroll
-        for (u32 h = 0; h < 2; h++) {
-          const h8 bv = *(const h8*)(Bs + (b * GM_BN + 32 * h + (l & 31)) * GM_LD + 16 * ks + 8 * (l >> 5));
-          acc[b][h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bv, acc[b][h], 0, 0, 0);
-        }
-    }
-    __syncthreads();
-  }
-  // epilogue: acc[..][i] is row 8 (i / 4) + 4 (l / 32) + i % 4 of the wave's 32, column l % 32
-#pragma unroll
-  for (u32 h = 0; h < 2; h++)
-#pragma unroll
-    for (u32 i = 0; i < 16; i++) {
-      const u32 row = 32 * w + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3), col = n0 + 32 * h + (l & 31);
-      if (m0 + row >= M) continue;
-      const u64 s = base + m0 + row;
-      if (MODE == 0) {
-        const float gv = acc[0][h][i], uv = acc[NB - 1][h][i];
-        ((_Float16*)g.out)[s * g.N + col] = (_Float16)(gv / (1.0f + __expf(-gv)) * uv);
-      } else {
-        ((float*)g.out)[s * g.N + col] = acc[0][h][i];
-      }
-    }
-}
-
-// ---- the pipelined grouped GEMM. Block tile: BM = 128 slots x 128 B rows (mode 0: 64 gate + 64 up
-// features, mode 1: 128 features), K in steps of 64, four waves of 64 x 64 (2 x 2 MFMA 32x32x16
+// ---- the grouped GEMM. Block tile: BM = 256 slots x 128 weight rows (mode 0: 64 gate + 64 up
+// features, mode 1: 128 features), K in steps of 64, eight waves of 64 x 64 (2 x 2 MFMA 32x32x16
 // tiles; in mode 0 one wave's gate and up tiles cover the same 32 features, so the SwiGLU epilogue
-// pairs them in registers). LDS holds two stages of A and B (f16, rows padded to 72 halves): while
-// the MFMAs run on one stage, the next tile's A rows and raw weight half-spans are in flight into
-// registers; after the MFMAs they are dequantized into the other stage. One barrier a k-tile.
+// pairs them in registers). A tile of 256 slots holds a whole expert at prefill sizes, so each weight
+// tile is read once. LDS holds two stages of A and B (f16, rows padded to 72 halves): while the
+// MFMAs run on one stage, the next three tiles' A rows and raw weight half-spans are in flight into
+// registers; after the MFMAs one tile is dequantized into the other stage. One barrier a k-tile.
 #define G2_BK 64
 #define G2_LD 72
-#define G2_STAGE (2 * GM_BM * G2_LD)  // halves: A [128][72] then B [128][72]
+#define G2_BN 128                                  // weight rows a tile
+#define G2_STAGE ((GM_BM + G2_BN) * G2_LD)         // halves: A [256][72] then B [128][72]
 
 // XCD-aware order: the hardware deals block b to XCD b % 8, so block b takes m-tile
 // 8 ((b / 8) / NT) + b % 8 and feature tile (b / 8) % NT: an m-tile's NT feature tiles all run on
 // one XCD and read its activation rows from that XCD's L2 (1-D grid, 8 NT ceil(tiles / 8) blocks)
 template <u32 F, u32 MODE>
-__global__ void __launch_bounds__(256, 2) k_moe_gemm2(GemmArgs g, u32 NT) {
+__global__ void __launch_bounds__(512) k_moe_gemm2(GemmArgs g, u32 NT) {
   extern __shared__ _Float16 lds[];
   const u32 bi = blockIdx.x >> 3, tile = 8 * (bi / NT) + (blockIdx.x & 7), ntile = bi % NT;
   u32 e, m0, base, M;
@@ -185,28 +90,30 @@ __global__ void __launch_bounds__(256, 2) k_moe_gemm2(GemmArgs g, u32 NT) {
   }
   constexpr u32 NF = MODE == 0 ? 64u : 128u;  // output features a block
   const u32 n0 = ntile * NF, tid = threadIdx.x, w = tid >> 6, l = tid & 63, wm = w >> 1, wn = w & 1;
-  // A: 128 rows x 64 halves a k-tile, 16-byte chunks c = tid + 256 i (i < 4): row c / 8, chunk c % 8
+  // A: 256 rows x 64 halves a k-tile, 16-byte chunks c = tid + 512 i (i < 4): row c / 8, chunk c % 8
   const _Float16* asrc[4];
   bool aok[4];
 #pragma unroll
   for (u32 i = 0; i < 4; i++) {
-    const u32 c = tid + 256 * i, r = c >> 3;
+    const u32 c = tid + 512 * i, r = c >> 3;
     aok[i] = m0 + r < M;
     const u64 s = base + m0 + (aok[i] ? r : 0u);
     const u64 src = MODE == 0 ? (g.xmap ? (u64)g.xmap[s] : s) : s;
     asrc[i] = g.A + src * g.K + 8 * (c & 7);
   }
-  // B: 128 rows x 64 columns a k-tile; thread: row tid / 2, span tid % 2 (two half-spans)
-  const u32 br = tid >> 1, bs = tid & 1;
+  // B: 128 rows x 64 columns a k-tile; thread: row tid / 4, span (tid / 2) % 2, half tid % 2
+  const u32 br = tid >> 2, bs = (tid >> 1) & 1, bj = tid & 1;
   const u8* brow;
   if (MODE == 0) brow = (br < 64 ? g.W0 + (u64)(n0 + br) * g.rb : g.W1 + (u64)(n0 + br - 64) * g.rb) + (u64)e * g.es;
   else brow = g.W0 + (u64)e * g.es + (u64)(n0 + br) * g.rb;
+  // a wave whose 64 rows are all past the expert's slots skips its MFMAs (wave-uniform)
+  const bool live = m0 + 64 * wm < M;
 
   // three register slots keep k-tiles t + 2 .. t + 4 in flight while tile t is multiplied (slot of
   // tile u: u % 3); compile-time slot choice keeps them in registers
   struct Slot {
     uint4 a[4];
-    Half<F> h[2];
+    Half<F> h;
   };
   Slot s0, s1, s2;
   const u32 nk = g.K / G2_BK;
@@ -215,8 +122,7 @@ __global__ void __launch_bounds__(256, 2) k_moe_gemm2(GemmArgs g, u32 NT) {
     const u32 k0 = t * G2_BK;
 #pragma unroll
     for (u32 i = 0; i < 4; i++) s.a[i] = aok[i] ? *(const uint4*)(asrc[i] + k0) : make_uint4(0, 0, 0, 0);
-    s.h[0].ld(brow, k0 + 32 * bs, 0);
-    s.h[1].ld(brow, k0 + 32 * bs, 1);
+    s.h.ld(brow, k0 + 32 * bs, bj);
   };
   auto store = [&](const Slot& s, u32 t) {
     _Float16* As = lds + (t & 1) * G2_STAGE;
@@ -224,17 +130,14 @@ __global__ void __launch_bounds__(256, 2) k_moe_gemm2(GemmArgs g, u32 NT) {
     const u32 k0 = t * G2_BK;
 #pragma unroll
     for (u32 i = 0; i < 4; i++) {
-      const u32 c = tid + 256 * i;
+      const u32 c = tid + 512 * i;
       *(uint4*)(As + (c >> 3) * G2_LD + 8 * (c & 7)) = s.a[i];
     }
-#pragma unroll
-    for (u32 j = 0; j < 2; j++) {
-      u32 o[8];
-      half_f16<F>(s.h[j], k0 + 32 * bs, j, o);
-      _Float16* d = Bs + br * G2_LD + 32 * bs + 16 * j;
-      *(uint4*)d = make_uint4(o[0], o[1], o[2], o[3]);
-      *(uint4*)(d + 8) = make_uint4(o[4], o[5], o[6], o[7]);
-    }
+    u32 o[8];
+    half_f16<F>(s.h, k0 + 32 * bs, bj, o);
+    _Float16* d = Bs + br * G2_LD + 32 * bs + 16 * bj;
+    *(uint4*)d = make_uint4(o[0], o[1], o[2], o[3]);
+    *(uint4*)(d + 8) = make_uint4(o[4], o[5], o[6], o[7]);
   };
 
   f32x16 acc[2][2];
@@ -247,6 +150,7 @@ __global__ void __launch_bounds__(256, 2) k_moe_gemm2(GemmArgs g, u32 NT) {
   // B rows of this wave's two 32-column tiles
   const u32 bro0 = MODE == 0 ? 32 * wn : 64 * wn, bro1 = MODE == 0 ? 64 + 32 * wn : 64 * wn + 32;
   auto mma = [&](u32 t) {
+    if (!live) return;
     const _Float16* As = lds + (t & 1) * G2_STAGE;
     const _Float16* Bs = As + GM_BM * G2_LD;
 #pragma unroll
@@ -324,53 +228,28 @@ __global__ void __launch_bounds__(256) k_combine(const float* __restrict__ out, 
 
 // ---------------------------------------------------------------- launchers
 
-size_t gemm_lds(u32 mode) { return ((size_t)GM_BM * GM_LD + (size_t)(mode == 0 ? 2 : 1) * GM_BN * GM_LD) * 2; }
-
-// more than 64 KiB of dynamic LDS has to be allowed per kernel (gfx950 has 160 KiB a CU)
-template <u32 F, u32 MODE> static void gemm_go(const GemmArgs& g, dim3 grid, size_t sm, hipStream_t st) {
-  static bool set = false;
-  if (!set) {
-    (void)hipFuncSetAttribute((const void*)k_moe_gemm<F, MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
-    set = true;
-  }
-  LAUNCH_K((k_moe_gemm<F, MODE>), grid, dim3(256), sm, st, g);
-}
-
 template <u32 F, u32 MODE> static void gemm2_go(const GemmArgs& g, dim3 grid, size_t sm, hipStream_t st) {
   static bool set = false;
   if (!set) {
     (void)hipFuncSetAttribute((const void*)k_moe_gemm2<F, MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
     set = true;
   }
-  LAUNCH_K((k_moe_gemm2<F, MODE>), grid, dim3(256), sm, st, g, g.N / (MODE == 0 ? 64u : 128u));
+  LAUNCH_K((k_moe_gemm2<F, MODE>), grid, dim3(512), sm, st, g, g.N / (MODE == 0 ? 64u : 128u));
 }
 
 int launch_moe_gemm(const GemmArgs& g, u32 fm, u32 mode, u32 grid_y, hipStream_t st) {
   const u32 nf = mode == 0 ? 64u : 128u;
-  if (g.K % G2_BK == 0 && g.N % nf == 0 && fm != FM_F32) {
-    const dim3 grid(8 * (g.N / nf) * ((grid_y + 7) / 8));
-    const size_t sm = (size_t)2 * G2_STAGE * 2;
+  if (g.K % G2_BK || g.N % nf || fm == FM_F32) return -1;
+  const dim3 grid(8 * (g.N / nf) * ((grid_y + 7) / 8));
+  const size_t sm = (size_t)2 * G2_STAGE * 2;
 #define G2_L(F) \
   if (fm == F) { \
     if (mode == 0) gemm2_go<F, 0>(g, grid, sm, st); \
     else gemm2_go<F, 1>(g, grid, sm, st); \
     return 0; \
   }
-    G2_L(FM_Q8_0) G2_L(FM_Q4_K) G2_L(FM_Q6_K) G2_L(FM_Q5_K)
+  G2_L(FM_Q8_0) G2_L(FM_Q4_K) G2_L(FM_Q6_K) G2_L(FM_Q5_K)
 #undef G2_L
-    return -1;
-  }
-  if (g.K % GM_BK || g.N % GM_BN) return -1;
-  const dim3 grid(g.N / GM_BN, grid_y);
-  const size_t sm = gemm_lds(mode);
-#define GM_L(F) \
-  if (fm == F) { \
-    if (mode == 0) gemm_go<F, 0>(g, grid, sm, st); \
-    else gemm_go<F, 1>(g, grid, sm, st); \
-    return 0; \
-  }
-  GM_L(FM_Q8_0) GM_L(FM_Q4_K) GM_L(FM_Q6_K) GM_L(FM_Q5_K)
-#undef GM_L
   return -1;
 }
 

@@ -119,7 +119,6 @@ struct GemmArgs {
   void* out;          // mode 0: f16 [slots][N]; mode 1: f32 [slots][N]
 };
 int launch_moe_gemm(const GemmArgs& g, uint32_t fm, uint32_t mode, uint32_t grid_y, hipStream_t st);
-size_t gemm_lds(uint32_t mode);
 uint32_t gemm_bm();
 int launch_to_f16(const float* x, _Float16* y, uint64_t n, hipStream_t st);
 int launch_tiles(const uint32_t* off, uint32_t ne, uint32_t* tiles, uint32_t* ntiles, hipStream_t st);
