@@ -365,6 +365,7 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
   g.K = L->dm;
   g.N = L->ef;
   g.A = x16;
+  g.arows = T;
   g.xmap = xmap;
   g.off = off;
   g.tiles = tiles;
@@ -381,6 +382,7 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
   d.K = L->ef;
   d.N = L->dm;
   d.A = (const _Float16*)(gb + gs.act);
+  d.arows = n;
   d.xmap = nullptr;
   d.out = gb + gs.out;
   stage_begin(ST_DN);
@@ -397,6 +399,7 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
     sg.N = L->sf;
     sg.M = T;
     sg.A = x16;
+    sg.arows = T;
     sg.out = gb + gs.sact;
     if ((rc = launched(launch_moe_gemm(sg, L->fsg, 0, mt, g_stream), "shared gate/up GEMM"))) return rc;
     GemmArgs sd{};
@@ -406,6 +409,7 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
     sd.N = L->dm;
     sd.M = T;
     sd.A = (const _Float16*)(gb + gs.sact);
+    sd.arows = T;
     sd.out = gb + gs.shd;
     if ((rc = launched(launch_moe_gemm(sd, L->fsd, 1, mt, g_stream), "shared down GEMM"))) return rc;
     shd = (const float*)(gb + gs.shd);

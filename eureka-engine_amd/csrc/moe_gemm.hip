@@ -90,16 +90,23 @@ __global__ void __launch_bounds__(512) k_moe_gemm2(GemmArgs g, u32 NT) {
   }
   constexpr u32 NF = MODE == 0 ? 64u : 128u;  // output features a block
   const u32 n0 = ntile * NF, tid = threadIdx.x, w = tid >> 6, l = tid & 63, wm = w >> 1, wn = w & 1;
-  // A: 256 rows x 64 halves a k-tile, 16-byte chunks c = tid + 512 i (i < 4): row c / 8, chunk c % 8
-  const _Float16* asrc[4];
-  bool aok[4];
+  // A: 256 rows x 64 halves a k-tile, 16-byte chunks c = tid + 512 i (i < 4): row c / 8, chunk c % 8.
+  // Buffer loads bounded by A's size: a row past the expert's slots gets an offset past the bound, so
+  // its load returns zeros without touching memory, and every load stays unconditional (a load under a
+  // branch makes the compiler wait for all of them)
+  const __amdgpu_buffer_rsrc_t arsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)g.A, (short)0, (int)(g.arows * g.K * 2u), 0x00020000);
+  u32 aoff[4], src[4];
+#pragma unroll
+  for (u32 i = 0; i < 4; i++) src[i] = base + m0 + min((tid + 512 * i) >> 3, M - m0 - 1);  // a live slot
+  if (MODE == 0 && g.xmap) {  // slot -> token row, the four reads in flight together
+#pragma unroll
+    for (u32 i = 0; i < 4; i++) src[i] = g.xmap[src[i]];
+  }
 #pragma unroll
   for (u32 i = 0; i < 4; i++) {
     const u32 c = tid + 512 * i, r = c >> 3;
-    aok[i] = m0 + r < M;
-    const u64 s = base + m0 + (aok[i] ? r : 0u);
-    const u64 src = MODE == 0 ? (g.xmap ? (u64)g.xmap[s] : s) : s;
-    asrc[i] = g.A + src * g.K + 8 * (c & 7);
+    aoff[i] = m0 + r < M ? (src[i] * g.K + 8 * (c & 7)) * 2u : 0x80000000u;
   }
   // B: 128 rows x 64 columns a k-tile; thread: row tid / 4, span (tid / 2) % 2, half tid % 2
   const u32 br = tid >> 2, bs = (tid >> 1) & 1, bj = tid & 1;
@@ -118,10 +125,12 @@ __global__ void __launch_bounds__(512) k_moe_gemm2(GemmArgs g, u32 NT) {
   Slot s0, s1, s2;
   const u32 nk = g.K / G2_BK;
   auto load = [&](Slot& s, u32 t) {
-    if (t >= nk) return;
-    const u32 k0 = t * G2_BK;
+    const u32 k0 = min(t, nk - 1) * G2_BK;  // past the end: a repeat of the last tile, never stored
 #pragma unroll
-    for (u32 i = 0; i < 4; i++) s.a[i] = aok[i] ? *(const uint4*)(asrc[i] + k0) : make_uint4(0, 0, 0, 0);
+    for (u32 i = 0; i < 4; i++) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(arsrc, (int)(aoff[i] + 2 * k0), 0, 0);
+      s.a[i] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
     s.h.ld(brow, k0 + 32 * bs, bj);
   };
   auto store = [&](const Slot& s, u32 t) {
@@ -167,13 +176,17 @@ __global__ void __launch_bounds__(512) k_moe_gemm2(GemmArgs g, u32 NT) {
     }
   };
   // iteration t: multiply tile t, store tile t + 1 (its slot) into the other stage, refill that
-  // slot with tile t + 4, one barrier
+  // slot with tile t + 4, one barrier. The steady-state loop runs while three tiles follow, so its
+  // stores and loads are unconditional; the last one to three iterations only multiply and store.
   auto step = [&](Slot& s, u32 t) {
     mma(t);
-    if (t + 1 < nk) {
-      store(s, t + 1);
-      load(s, t + 4);
-    }
+    store(s, t + 1);
+    load(s, t + 4);
+    __syncthreads();
+  };
+  auto tail = [&](const Slot& s, u32 t) {
+    mma(t);
+    if (t + 1 < nk) store(s, t + 1);
     __syncthreads();
   };
   load(s0, 0);
@@ -183,13 +196,15 @@ __global__ void __launch_bounds__(512) k_moe_gemm2(GemmArgs g, u32 NT) {
   load(s0, 3);
   __syncthreads();
   u32 t = 0;
-  for (; t + 3 <= nk; t += 3) {
+  for (; t + 4 <= nk; t += 3) {
     step(s1, t);
     step(s2, t + 1);
     step(s0, t + 2);
   }
-  if (t < nk) step(s1, t);
-  if (t + 1 < nk) step(s2, t + 1);
+  // 1 .. 3 tiles left; their slots continue the rotation
+  tail(s1, t);
+  if (t + 1 < nk) tail(s2, t + 1);
+  if (t + 2 < nk) tail(s0, t + 2);
   // epilogue: acc[a][b][i] is row 64 wm + 32 a + 8 (i / 4) + 4 (l / 32) + i % 4 of the tile,
   // column l % 32 of B tile b
 #pragma unroll
@@ -239,7 +254,8 @@ template <u32 F, u32 MODE> static void gemm2_go(const GemmArgs& g, dim3 grid, si
 
 int launch_moe_gemm(const GemmArgs& g, u32 fm, u32 mode, u32 grid_y, hipStream_t st) {
   const u32 nf = mode == 0 ? 64u : 128u;
-  if (g.K % G2_BK || g.N % nf || fm == FM_F32) return -1;
+  // A's buffer loads take 32-bit offsets below 2^31 (dead rows use 2^31)
+  if (g.K % G2_BK || g.N % nf || fm == FM_F32 || (u64)g.arows * g.K * 2 >= (1ull << 31)) return -1;
   const dim3 grid(8 * (g.N / nf) * ((grid_y + 7) / 8));
   const size_t sm = (size_t)2 * G2_STAGE * 2;
 #define G2_L(F) \

@@ -111,6 +111,7 @@ struct GemmArgs {
   const uint8_t* W1;  // up (mode 0)
   uint64_t es, rb;    // expert stride, row bytes
   uint32_t K, N, M;   // M: rows when there is no tile list (the shared expert)
+  uint32_t arows;     // rows of A (the bound of its buffer loads)
   const _Float16* A;  // activations, f16 rows of K
   const uint32_t* xmap;   // slot -> A row (mode 0), or null: slot itself
   const uint32_t* off;    // [ne + 1] slot offsets
