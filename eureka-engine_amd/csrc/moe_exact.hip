@@ -151,6 +151,75 @@ __global__ void __launch_bounds__(64) k_tree_rows(TreeArgs a) {
   BSTAMP(0, 1);
 }
 
+// Many tokens (prefill, batches): a block of four waves takes 8 consecutive rows and TT tokens. The
+// tokens' x rows are staged in LDS once (coalesced loads, lanes padded 4 floats apart); each wave holds
+// its two rows' weights in registers (lane L: the contiguous leaves [NQ L, NQ L + NQ)) and reduces
+// them against every token: the in-lane levels, then tree64_asc -- the same tree as tree_body, so the
+// same sums. Weights are read once a token tile instead of once a token.
+template <u32 NSP, u32 TT>
+__global__ void __launch_bounds__(256) k_tree_rows_mt(TreeArgs a) {
+  constexpr u32 NQ = 8 * NSP, LS = 4 * NQ + 4;
+  extern __shared__ float xsh[];  // [TT][64 lanes][LS]
+  const u32 tid = threadIdx.x, w = tid >> 6, L = tid & 63;
+  const u32 t0 = blockIdx.y * TT, nl4 = a.cols / 4;
+  // x of the tile's tokens (tokens past T are zeros): all sixteen loads a thread in flight, then the
+  // stores
+  static_assert(TT * 64 * NQ == 16 * 256, "sixteen float4 a thread");
+  float4 xl[16];
+#pragma unroll
+  for (u32 j = 0; j < 16; j++) {
+    const u32 i = tid + 256 * j, tt = i / (64 * NQ), li = i % (64 * NQ), t = t0 + tt;
+    xl[j] = (t < a.T && li < nl4) ? ((const float4*)(a.x + (u64)t * a.xstride))[li] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (u32 j = 0; j < 16; j++) {
+    const u32 i = tid + 256 * j, tt = i / (64 * NQ), li = i % (64 * NQ);
+    *(float4*)(xsh + tt * 64 * LS + (li / NQ) * LS + 4 * (li % NQ)) = xl[j];
+  }
+  // this wave's two rows
+  const u32 c0 = 32 * NSP * L;
+  const bool live = c0 < a.cols;
+  u32 row[2], sgi[2];
+#pragma unroll
+  for (u32 k = 0; k < 2; k++) {
+    u32 r = blockIdx.x * 8 + 2 * w + k, s = 0;
+    while (s < a.nseg && r >= a.seg[s].rows) { r -= a.seg[s].rows; s++; }
+    row[k] = r;
+    sgi[k] = s;  // nseg: past the last row
+  }
+  float wr[2][32 * NSP];
+#pragma unroll
+  for (u32 k = 0; k < 2; k++) {
+    const bool ok = live && sgi[k] < a.nseg;
+#pragma unroll
+    for (u32 q = 0; q < NSP; q++) {
+      if (ok) {
+        const TreeSeg& sg = a.seg[sgi[k]];
+        span_any(sg.fm, sg.W + (u64)row[k] * sg.rb, c0 + 32 * q, wr[k] + 32 * q);
+      } else {
+#pragma unroll
+        for (u32 i = 0; i < 32; i++) wr[k][32 * q + i] = 0.0f;
+      }
+    }
+  }
+  __syncthreads();
+  for (u32 tt = 0; tt < TT && t0 + tt < a.T; tt++) {
+    float4 xv[NQ];
+#pragma unroll
+    for (u32 q = 0; q < NQ; q++) xv[q] = *(const float4*)(xsh + tt * 64 * LS + L * LS + 4 * q);
+#pragma unroll
+    for (u32 k = 0; k < 2; k++) {
+      if (sgi[k] >= a.nseg) continue;
+      float n[NQ];
+#pragma unroll
+      for (u32 q = 0; q < NQ; q++) n[q] = leaf4(wr[k] + 4 * q, xv[q]);
+      const float v = tree64_asc(live ? tree_in_lane<NQ>(n) : 0.0f);  // a dead lane's leaves are +0 pads
+      const TreeSeg& sg = a.seg[sgi[k]];
+      if (L == 0) sg.out[(u64)(t0 + tt) * sg.ostride + row[k]] = sg.bias ? v + sg.bias[row[k]] : v;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- top-k (llb_moe_topk)
 
 // (value, index) of the larger p, ties to the lower index
@@ -901,6 +970,20 @@ int launch_tree_rows(const TreeArgs& a, u32 nsp, hipStream_t st) {
   u32 rows = 0;
   for (u32 i = 0; i < a.nseg; i++) rows += a.seg[i].rows;
   if (rows == 0) return 0;
+  if (a.T >= 16 && nsp <= 2) {  // token tiles: weights read once a tile
+    const u32 tt = nsp == 1 ? 8u : 4u;
+    const size_t sm = (size_t)tt * 64 * (32 * nsp + 4) * 4;
+    const dim3 grid((rows + 7) / 8, (a.T + tt - 1) / tt);
+    static bool set1 = false, set2 = false;
+    if (nsp == 1) {
+      if (!set1) { (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<1, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm); set1 = true; }
+      LAUNCH_K((k_tree_rows_mt<1, 8>), grid, dim3(256), sm, st, a);
+    } else {
+      if (!set2) { (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<2, 4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm); set2 = true; }
+      LAUNCH_K((k_tree_rows_mt<2, 4>), grid, dim3(256), sm, st, a);
+    }
+    return 0;
+  }
   const u32 rpw = tree_rows_per_wave(nsp);
   dim3 grid((rows + rpw - 1) / rpw, a.T);
   if (nsp == 1) { LAUNCH_K((k_tree_rows<1>), grid, dim3(64), 0, st, a); return 0; }

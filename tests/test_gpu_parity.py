@@ -87,6 +87,15 @@ def test_exact_small_bit_exact(dev, si, fused):
     assert np.array_equal(y.view(np.uint32), yr.view(np.uint32)), float(np.abs(y - yr).max())
 
 
+@pytest.mark.parametrize("si", [0, 2, 3, 4])
+def test_exact_many_tokens_bit_exact(dev, si):
+    """T >= 16 takes the token-tiled router (one or two spans a lane, pad leaves for 1536 columns)."""
+    y, ids, wt, yr, idr, wtr, _, _ = _exact_case(dev, SMALL[si], seed=200 + si, T=20)
+    assert np.array_equal(ids, idr)
+    assert np.array_equal(wt.view(np.uint32), wtr.view(np.uint32))
+    assert np.array_equal(y.view(np.uint32), yr.view(np.uint32)), float(np.abs(y - yr).max())
+
+
 @pytest.mark.parametrize("name,seed,fused", [("c1", 0, False), ("c2", 0, False), ("c2", 1, False), ("c1k", 3, False),
                                              ("c5", 0, False),
                                              pytest.param("c2", 5, True, marks=pytest.mark.skip(reason=FUSED_SKIP))])
