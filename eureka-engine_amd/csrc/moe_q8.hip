@@ -36,40 +36,47 @@ int launch_q8_1(const float* x, uint32_t n, int8_t* q, float2* ds, hipStream_t s
 
 // block e of ne: off[e] = #{slots with id < e}; then e's slots in ascending slot order, each
 // wave's ballot giving a slot its rank: xmap[pos] = slot / nk, inv[slot] = pos. Deterministic.
+// the dispatch permutation (llb_mx_group, host/llb_pf.cuh:774-817): slots of expert e in slot order.
+// Block e; thread t scans the contiguous slots [t per, t per + per): ids below e (the expert's offset)
+// and equal to e (its hits); an exclusive scan of the hits over the block gives each thread its first
+// position, and it writes its hits in slot order -- the stable order, with one scan a block.
 __global__ void __launch_bounds__(256) k_group(const u32* __restrict__ ids, u32 n, u32 nk, u32 ne, u32* __restrict__ off,
                                                u32* __restrict__ xmap, u32* __restrict__ inv) {
-  __shared__ u32 wc[4];
-  __shared__ u32 base;
+  __shared__ u32 wl[4], wh[4];
   const u32 e = blockIdx.x, t = threadIdx.x, w = t >> 6, L = t & 63;
-  u32 lt = 0;
-  for (u32 i = t; i < n; i += 256) lt += ids[i] < e ? 1u : 0u;
+  const u32 per = (n + 255) / 256, i0 = min(t * per, n), i1 = min(i0 + per, n);
+  u32 lt = 0, hit = 0;
+  for (u32 i = i0; i < i1; i++) {
+    const u32 v = ids[i];
+    lt += v < e ? 1u : 0u;
+    hit += v == e ? 1u : 0u;
+  }
+  // inclusive scan of hit across the wave, sum of lt
+  u32 inc = hit, lsum = lt;
 #pragma unroll
-  for (u32 m = 32; m > 0; m >>= 1) lt += __shfl_xor(lt, m, 64);
-  if (L == 0) wc[w] = lt;
+  for (u32 m = 1; m < 64; m <<= 1) {
+    const u32 o = __shfl_up(inc, m, 64);
+    if (L >= m) inc += o;
+    lsum += __shfl_xor(lsum, m, 64);
+  }
+  if (L == 63) wh[w] = inc;
+  if (L == 0) wl[w] = lsum;
   __syncthreads();
+  const u32 base = wl[0] + wl[1] + wl[2] + wl[3];
+  u32 pos = base + inc - hit;
+  for (u32 k = 0; k < w; k++) pos += wh[k];
   if (t == 0) {
-    base = wc[0] + wc[1] + wc[2] + wc[3];
     off[e] = base;
     if (e + 1 == ne) off[ne] = n;
   }
-  __syncthreads();
-  for (u32 i0 = 0; i0 < n; i0 += 256) {
-    const u32 i = i0 + t;
-    const bool hit = i < n && ids[i] == e;
-    const u64 bal = __ballot(hit);
-    __syncthreads();
-    if (L == 0) wc[w] = (u32)__popcll(bal);
-    __syncthreads();
-    u32 before = base;
-    for (u32 k = 0; k < w; k++) before += wc[k];
-    const u32 at = before + (u32)__popcll(bal & ((1ull << L) - 1ull));
-    if (hit) {
-      xmap[at] = i / nk;
-      inv[i] = at;
+  if (hit) {
+    for (u32 i = i0; i < i1; i++) {
+      if (ids[i] == e) {
+        xmap[pos] = i / nk;
+        inv[i] = pos;
+        pos++;
+      }
     }
-    __syncthreads();
-    if (t == 0) base += wc[0] + wc[1] + wc[2] + wc[3];
-    __syncthreads();
   }
 }
 
