@@ -229,16 +229,45 @@ __global__ void __launch_bounds__(256) k_combine(const float* __restrict__ out, 
                                                  const float* __restrict__ wt, u32 nk, const float* __restrict__ shd,
                                                  const float* __restrict__ sgo, const float* __restrict__ x1,
                                                  float* __restrict__ y, u32 dm) {
-  const u32 t = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
+  // four outputs a thread (dm % 4 == 0); the token's slot rows and weights read once into LDS; the
+  // slot values of up to eight ranks in flight at once, summed in rank order
+  __shared__ u32 srow[64];
+  __shared__ float swt[64];
+  const u32 t = blockIdx.y, r = 4 * (blockIdx.x * 256 + threadIdx.x);
+  if (threadIdx.x < nk) {
+    srow[threadIdx.x] = inv[(u64)t * nk + threadIdx.x];
+    swt[threadIdx.x] = wt[(u64)t * nk + threadIdx.x];
+  }
+  __syncthreads();
   if (r >= dm) return;
-  float mo = 0.0f;
-  for (u32 j = 0; j < nk; j++) {
-    const float v = out[(u64)inv[(u64)t * nk + j] * dm + r];
-    mo = j == 0 ? v * wt[(u64)t * nk] : mo + v * wt[(u64)t * nk + j];
+  float4 mo = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (u32 j0 = 0; j0 < nk; j0 += 8) {
+    float4 v[8];
+#pragma unroll
+    for (u32 j = 0; j < 8; j++)
+      if (j0 + j < nk) v[j] = *(const float4*)(out + (u64)srow[j0 + j] * dm + r);
+#pragma unroll
+    for (u32 j = 0; j < 8; j++) {
+      if (j0 + j >= nk) break;
+      const float w = swt[j0 + j];
+      if (j0 + j == 0) {
+        mo = make_float4(v[j].x * w, v[j].y * w, v[j].z * w, v[j].w * w);
+      } else {
+        mo.x = mo.x + v[j].x * w; mo.y = mo.y + v[j].y * w; mo.z = mo.z + v[j].z * w; mo.w = mo.w + v[j].w * w;
+      }
+    }
   }
   const u64 o = (u64)t * dm + r;
-  const float res = x1 ? x1[o] : 0.0f;
-  y[o] = shd ? (mo + shd[o] * sgo[t]) + res : mo + res;
+  const float4 res = x1 ? *(const float4*)(x1 + o) : make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 yv;
+  if (shd) {
+    const float4 s = *(const float4*)(shd + o);
+    const float g = sgo[t];
+    yv = make_float4((mo.x + s.x * g) + res.x, (mo.y + s.y * g) + res.y, (mo.z + s.z * g) + res.z, (mo.w + s.w * g) + res.w);
+  } else {
+    yv = make_float4(mo.x + res.x, mo.y + res.y, mo.z + res.z, mo.w + res.w);
+  }
+  *(float4*)(y + o) = yv;
 }
 
 // ---------------------------------------------------------------- launchers
@@ -279,7 +308,8 @@ int launch_tiles(const u32* off, u32 ne, u32* tiles, u32* ntiles, hipStream_t st
 }
 int launch_combine(const float* out, const u32* inv, const float* wt, u32 nk, const float* shd, const float* sgo,
                    const float* x1, float* y, u32 dm, u32 T, hipStream_t st) {
-  hipLaunchKernelGGL(k_combine, dim3((dm + 255) / 256, T), dim3(256), 0, st, out, inv, wt, nk, shd, sgo, x1, y, dm);
+  if (dm % 4 || nk > 64) return -1;
+  hipLaunchKernelGGL(k_combine, dim3((dm / 4 + 255) / 256, T), dim3(256), 0, st, out, inv, wt, nk, shd, sgo, x1, y, dm);
   return 0;
 }
 u32 gemm_bm() { return GM_BM; }
