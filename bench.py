@@ -1,7 +1,7 @@
-"""Benchmark of the MoE FFN hot path on one MI355X (BASELINE.json metric: MoE layer us/token at
+"""Benchmark of the MoE FFN hot path on one MI355X (headline metric: MoE layer us/token at
 decode + prefill tok/s, each against the HBM / MFMA roofline).
 
-Default workload: the Qwen3.5-35B-A3B-like layer -- hidden 2048, 256 experts,
+Default workload (single-token decode): the Qwen3.5-35B-A3B-like layer -- hidden 2048, 256 experts,
 top-8, expert ff 512, shared expert 512, gate/up Q4_K, down Q6_K -- decoding one token through
 40 independently seeded layers resident in HBM (about 21 GB of expert stacks, far past the caches).
 A step = one token through the 40 layers; value = microseconds per token-layer.
@@ -153,6 +153,8 @@ def main():
     ap.add_argument("--no-prefill", dest="prefill", action="store_false", help="skip the prefill leg")
     ap.add_argument("--prefill-config", default="c1")
     ap.add_argument("--prefill-T", type=int, default=2048)
+    ap.add_argument("--no-c5", dest="c5", action="store_false",
+                    help="skip the config-5 leg (48 resident 512-expert layers, 1 + 512 tokens a launch)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run three 256 MiB device-to-device copies (the PMC byte-counter calibration) and exit")
     args = ap.parse_args()
@@ -259,6 +261,13 @@ def main():
         # the same layer shape with Q4_K gate / up and Q6_K down weight tiles
         out["prefill_k_quants"] = prefill(dev, em.SHAPES["c1k"], args.prefill_T, 4, max(2, args.steps // 4), 1, "c1k")
         out["prefill_k_quants"]["config"] = f"c1k layer (Q4_K gate/up, Q6_K down), {args.prefill_T}-token chunk, f16 MFMA tier"
+    if args.c5:
+        # config 5: one decode token and a 512-token chunk in one launch, Zipf(1.1) routing, 48 resident
+        # layers (512 experts, top-10, ~1 GB each) cycled layer by layer
+        c5 = batched(dev, em.SHAPES["c5"], 513, 48, 2, 1, em.F16)
+        c5["tokens_per_s"] = round(513 / (c5["us_per_layer"] * 1e-6), 1)
+        c5["config"] = "c5: 48 layers x 512 experts top-10 (Q4_K gate/up, Q6_K down, shared expert), 1 + 512 tokens a launch, f16 tier"
+        out["c5_mixed"] = c5
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(shape)
     print(json.dumps(out), flush=True)

@@ -174,7 +174,7 @@ class Device:
         return f.value, t.value
 
 
-# ---------------------------------------------------------------- layer shapes
+# ---------------------------------------------------------------- layer shapes (benchmark workloads)
 
 class Shape:
     def __init__(self, dm, ne, nk, ef, sf, fg, fu, fd, fsg=Q4_K, fsu=Q4_K, fsd=Q6_K, fused=False):
@@ -218,7 +218,7 @@ W_SIGMA = 0.02
 
 
 def zipf_bias(ne, seed, s=1.1):
-    """BASELINE config 3's skew: b_e = log z_e, z proportional to rank^-s over a seeded expert
+    """Expert-load skew of the batched-decode workload: b_e = log z_e, z proportional to rank^-s over a seeded expert
     permutation (ranks 1..ne), as f32"""
     rank = np.empty(ne, np.int64)
     rank[np.random.default_rng(seed).permutation(ne)] = np.arange(1, ne + 1)

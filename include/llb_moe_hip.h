@@ -80,7 +80,7 @@ typedef struct {
   llb_dptr G, U, D;    /* expert stacks; U ignored when fused (U = G + ef rows, llb_host.c:677) */
   llb_dptr SG, SU, SD; /* shared expert */
   llb_dptr router_bias; /* F32 [ne] added to each router logit, one rounding (0: none). Not in the
-                         * reference: BASELINE config 3 skews expert load with it */
+                         * reference: the batched-decode workload skews expert load with it */
 } llb_moe_layer;
 
 /* ---- the layer's table row (host code) ----

@@ -45,7 +45,7 @@ typedef struct {
   const uint8_t* SG;             /* [sf] rows of dm cols */
   const uint8_t* SU;             /* [sf] rows of dm cols */
   const uint8_t* SD;             /* [dm] rows of sf cols */
-  const float* router_bias;      /* [ne] added to each logit (NULL: none); BASELINE config 3's skew */
+  const float* router_bias;      /* [ne] added to each logit (NULL: none); batched-decode expert skew */
 } mo_layer;
 
 /* ---- formats ---- */

@@ -314,6 +314,28 @@ def test_f16_tier_prefill_2048_sampled(dev):
     assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
 
 
+def test_f16_tier_config5_mixed(dev):
+    """config 5: 512 experts top-10 with the shared expert, one decode token plus a 512-token chunk in one
+    launch, Zipf(1.1) router bias; token 0 and 15 others checked against the oracle (routing bit-exact)"""
+    shape, T, seed = em.SHAPES["c5"], 513, 5
+    bias = em.zipf_bias(shape.ne, seed)
+    _say("f16 tier c5 mixed", "T", T)
+    layer = em.Layer(dev, shape, seed=seed, bias=bias)
+    run = em.Runner(dev, shape, T, tier=em.F16)
+    run.gen_inputs(seed)
+    run.forward(layer, residual=False)
+    y, ids, wt = run.outputs()
+    run.free()
+    layer.free()
+    h2, _ = ol.inputs(shape, seed, T)
+    toks = np.concatenate([[0], np.random.default_rng(seed).choice(np.arange(1, T), 15, replace=False)])
+    yr, idr, wtr, _ = ol.HostLayer(shape, seed=seed, experts=[], bias=bias).run(h2[toks], None)
+    assert np.array_equal(ids[toks], idr)
+    assert np.array_equal(wt[toks].view(np.uint32), wtr.view(np.uint32))
+    m = ol.err_metrics(y[toks], yr)
+    assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
+
+
 @pytest.mark.parametrize("tier", [em.EXACT, em.F16, em.Q8])
 def test_batched_zipf_config3(dev, tier):
     """config 3: 64 tokens through the config-1 layer with a Zipf(1.1) router bias (skewed loads)"""
