@@ -7,6 +7,9 @@ top-8, expert ff 512, shared expert 512, gate/up Q4_K, down Q6_K -- decoding one
 A step = one token through the 40 layers; value = microseconds per token-layer.
 
   python bench.py [--steps K] [--warmup W] [--layers L] [--config c2] [--tier exact|q8] [--no-cpu]
+                  [--legs batched,prefill,prefill_k,c5]
+  python bench.py --copy-calib          (the PMC byte-counter calibration copies only)
+  python bench.py --traffic-from DIR    (profiles/traffic.json from rocprofv3 FETCH_SIZE / WRITE_SIZE passes)
 """
 import argparse
 import ctypes as C
@@ -33,6 +36,64 @@ def measured_traffic(workload, stage, applies=True):
             return json.load(f)[workload][stage] if applies else None
     except (OSError, KeyError, ValueError):
         return None
+
+
+# kernel (rocprofv3 name prefix) -> (workload, stage) for the PMC passes run with --legs prefill,prefill_k;
+# the GEMM's first template argument is the weight format (1 Q8_0, 3 Q4_K, 4 Q6_K), its second the mode
+TRAFFIC_KERNELS = {
+    "k_tree_rows<": ("c2_decode", "route"),
+    "k_gu_topk<": ("c2_decode", "gate_up"),
+    "k_dn_lane<": ("c2_decode", "down"),
+    "k_moe_gemm2<1u, 0u>": ("c1_prefill_2048", "gate_up"),
+    "k_moe_gemm2<1u, 1u>": ("c1_prefill_2048", "down"),
+    "k_moe_gemm2<3u, 0u>": ("c1k_prefill_2048", "gate_up"),
+    "k_moe_gemm2<4u, 1u>": ("c1k_prefill_2048", "down"),
+}
+
+
+def _counter_means(d, counter, prefix=None):
+    """mean value of `counter` per dispatch for each kernel in a rocprofv3 --pmc csv directory."""
+    import csv
+    import glob
+    fs = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not fs:
+        raise SystemExit(f"bench.py: no counter_collection.csv under {d}")
+    acc = {}
+    for f in fs:
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] != counter:
+                continue
+            name = r["Kernel_Name"].removeprefix("void ").removeprefix("__amd_rocclr_")
+            key = next((k for k in (prefix or TRAFFIC_KERNELS) if name.startswith(k)), None)
+            if key is None:
+                continue
+            # a dispatch's counter can be split over rows (one per XCD / instance): sum by dispatch first
+            acc.setdefault(key, {}).setdefault(r["Dispatch_Id"], 0.0)
+            acc[key][r["Dispatch_Id"]] += float(r["Counter_Value"])
+    return {k: sum(v.values()) / len(v) for k, v in acc.items()}
+
+
+def traffic_from(d):
+    """profiles/traffic.json from DIR/{pmc,cal}_{FETCH_SIZE,WRITE_SIZE}: per-launch HBM bytes of each stage
+    kernel, each counter scaled by what it reads for the --copy-calib copies (256 MiB each)."""
+    cal_kib = (256 << 20) / 1024
+    cf = _counter_means(os.path.join(d, "cal_FETCH_SIZE"), "FETCH_SIZE", ["copyBuffer"])["copyBuffer"]
+    cw = _counter_means(os.path.join(d, "cal_WRITE_SIZE"), "WRITE_SIZE", ["copyBuffer"])["copyBuffer"]
+    ff, wf = cal_kib / cf, cal_kib / cw
+    fe = _counter_means(os.path.join(d, "pmc_FETCH_SIZE"), "FETCH_SIZE")
+    wr = _counter_means(os.path.join(d, "pmc_WRITE_SIZE"), "WRITE_SIZE")
+    out = {"method": "rocprofv3 --pmc FETCH_SIZE, then --pmc WRITE_SIZE (KiB per dispatch, averaged over "
+                     "dispatches); bytes = FETCH_SIZE * fetch_factor * 1024 + WRITE_SIZE * write_factor * 1024, "
+                     "the factors from 256 MiB device-to-device copies (bench.py --copy-calib) profiled the same way",
+           "fetch_factor": round(ff, 4), "write_factor": round(wf, 4),
+           "calibration_kib": {"fetch": cf, "write": cw}, "kib_per_dispatch": {}}
+    for k, (wl, st) in TRAFFIC_KERNELS.items():
+        if k in fe and k in wr:
+            out.setdefault(wl, {})[st] = int(round((fe[k] * ff + wr[k] * wf) * 1024))
+            out["kib_per_dispatch"][k] = {"fetch": round(fe[k], 1), "write": round(wr[k], 1)}
+    with open(os.path.join(ROOT, "profiles", "traffic.json"), "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out, indent=1))
 
 
 def stage_bytes(shape, T=1):
@@ -155,6 +216,10 @@ def main():
     ap.add_argument("--prefill-T", type=int, default=2048)
     ap.add_argument("--no-c5", dest="c5", action="store_false",
                     help="skip the config-5 leg (48 resident 512-expert layers, 1 + 512 tokens a launch)")
+    ap.add_argument("--legs", default="batched,prefill,prefill_k,c5",
+                    help="legs after the decode line: batched (config 3), prefill (c1), prefill_k (c1k), c5")
+    ap.add_argument("--traffic-from", metavar="DIR",
+                    help="only write profiles/traffic.json from the PMC csv directories under DIR and exit")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run three 256 MiB device-to-device copies (the PMC byte-counter calibration) and exit")
     args = ap.parse_args()
@@ -162,6 +227,14 @@ def main():
         print("bench.py: this build measures one GPU only (the MoE path is not sharded across GPUs); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.traffic_from:
+        traffic_from(args.traffic_from)
+        return
+    legs = set(args.legs.split(",")) if args.legs else set()
+    if not args.prefill:
+        legs -= {"batched", "prefill", "prefill_k"}
+    if not args.c5:
+        legs.discard("c5")
     if args.copy_calib:
         dev = em.Device(0)
         n = 256 << 20
@@ -247,21 +320,23 @@ def main():
                      "traffic": measured_traffic(f"{args.config}_decode", dom, args.tier == "exact"),
                      "bytes_per_launch": sbytes[dom], "kernel_us": round(dom_us, 3)},
     }
-    if args.prefill:
+    if "batched" in legs:
         b3 = {}
         for tn, tv in (("f16", em.F16), ("exact", em.EXACT)):
             b3[tn] = batched(dev, em.SHAPES["c1"], 64, 4, max(2, args.steps // 4), 1, tv)
         out["batched_c3"] = b3
-        for L in layers:
-            L.free()
-        layers.clear()
+    for L in layers:
+        L.free()
+    layers.clear()
+    if "prefill" in legs:
         pshape = em.SHAPES[args.prefill_config]
         out["prefill"] = prefill(dev, pshape, args.prefill_T, 4, max(2, args.steps // 4), 1, args.prefill_config)
         out["prefill"]["config"] = f"{args.prefill_config} layer, {args.prefill_T}-token chunk, f16 MFMA tier"
+    if "prefill_k" in legs:
         # the same layer shape with Q4_K gate / up and Q6_K down weight tiles
         out["prefill_k_quants"] = prefill(dev, em.SHAPES["c1k"], args.prefill_T, 4, max(2, args.steps // 4), 1, "c1k")
         out["prefill_k_quants"]["config"] = f"c1k layer (Q4_K gate/up, Q6_K down), {args.prefill_T}-token chunk, f16 MFMA tier"
-    if args.c5:
+    if "c5" in legs:
         # config 5: one decode token and a 512-token chunk in one launch, Zipf(1.1) routing, 48 resident
         # layers (512 experts, top-10, ~1 GB each) cycled layer by layer
         c5 = batched(dev, em.SHAPES["c5"], 513, 48, 2, 1, em.F16)

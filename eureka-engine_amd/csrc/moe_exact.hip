@@ -151,71 +151,102 @@ __global__ void __launch_bounds__(64) k_tree_rows(TreeArgs a) {
   BSTAMP(0, 1);
 }
 
-// Many tokens (prefill, batches): a block of four waves takes 8 consecutive rows and TT tokens. The
-// tokens' x rows are staged in LDS once (coalesced loads, lanes padded 4 floats apart); each wave holds
+// Many tokens (prefill, batches): a block of four waves takes 8 consecutive rows and tiles of TT tokens.
+// A tile's x rows are staged in LDS once (coalesced loads, lanes padded 4 floats apart); each wave holds
 // its two rows' weights in registers (lane L: the contiguous leaves [NQ L, NQ L + NQ)) and reduces
 // them against every token: the in-lane levels, then tree64_asc -- the same tree as tree_body, so the
-// same sums. Weights are read once a token tile instead of once a token.
+// same sums.
+// A block walks `ntb` consecutive tiles of TT tokens (grid.y = ceil(T / (TT ntb))) with its rows'
+// weights held in registers the whole time: weights are read once per TT ntb tokens, and the next
+// tile's x loads are in flight while the current tile is reduced. The wave index is made uniform so
+// the segment table and the row pointers come through scalar loads, ahead of every vector load.
 template <u32 NSP, u32 TT>
-__global__ void __launch_bounds__(256) k_tree_rows_mt(TreeArgs a) {
-  constexpr u32 NQ = 8 * NSP, LS = 4 * NQ + 4;
-  extern __shared__ float xsh[];  // [TT][64 lanes][LS]
-  const u32 tid = threadIdx.x, w = tid >> 6, L = tid & 63;
-  const u32 t0 = blockIdx.y * TT, nl4 = a.cols / 4;
-  // x of the tile's tokens (tokens past T are zeros): all sixteen loads a thread in flight, then the
-  // stores
-  static_assert(TT * 64 * NQ == 16 * 256, "sixteen float4 a thread");
-  float4 xl[16];
+DEV void tree_mt_load_x(const TreeArgs& a, u32 tid, u32 t0, float4* xl) {
+  constexpr u32 NQ = 8 * NSP;
+  const u32 nl4 = a.cols / 4;
 #pragma unroll
-  for (u32 j = 0; j < 16; j++) {
+  for (u32 j = 0; j < 16; j++) {  // tokens past T and columns past cols are zeros
     const u32 i = tid + 256 * j, tt = i / (64 * NQ), li = i % (64 * NQ), t = t0 + tt;
     xl[j] = (t < a.T && li < nl4) ? ((const float4*)(a.x + (u64)t * a.xstride))[li] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-#pragma unroll
-  for (u32 j = 0; j < 16; j++) {
-    const u32 i = tid + 256 * j, tt = i / (64 * NQ), li = i % (64 * NQ);
-    *(float4*)(xsh + tt * 64 * LS + (li / NQ) * LS + 4 * (li % NQ)) = xl[j];
-  }
-  // this wave's two rows
+}
+template <u32 NSP, u32 TT>
+__global__ void __launch_bounds__(256) k_tree_rows_mt(TreeArgs a, u32 ntb) {
+  constexpr u32 NQ = 8 * NSP, LS = 4 * NQ + 4;
+  static_assert(TT * 64 * NQ == 16 * 256, "sixteen float4 a thread");
+  constexpr u32 LS4 = LS / 4;
+  extern __shared__ float4 xsh4[];  // [TT][64 lanes][LS floats]
+  const u32 tid = threadIdx.x, L = tid & 63;
+  const u32 w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // this wave's two rows: segment, row in it, output and bias (wave-uniform)
   const u32 c0 = 32 * NSP * L;
   const bool live = c0 < a.cols;
-  u32 row[2], sgi[2];
+  const u8* wp[2];
+  float* op[2];
+  u32 fm[2], ost[2];
+  bool has[2], hb[2];
+  float bia[2];
 #pragma unroll
   for (u32 k = 0; k < 2; k++) {
     u32 r = blockIdx.x * 8 + 2 * w + k, s = 0;
     while (s < a.nseg && r >= a.seg[s].rows) { r -= a.seg[s].rows; s++; }
-    row[k] = r;
-    sgi[k] = s;  // nseg: past the last row
+    has[k] = s < a.nseg;  // false: past the last row
+    const TreeSeg& sg = a.seg[has[k] ? s : 0];
+    wp[k] = sg.W + (u64)r * sg.rb;
+    fm[k] = sg.fm;
+    op[k] = sg.out + r;
+    ost[k] = sg.ostride;
+    hb[k] = has[k] && sg.bias;
+    bia[k] = hb[k] ? sg.bias[r] : 0.0f;
+    has[k] = has[k] && sg.out != nullptr;
   }
+  const u32 tb = blockIdx.y * TT * ntb;
   float wr[2][32 * NSP];
 #pragma unroll
   for (u32 k = 0; k < 2; k++) {
-    const bool ok = live && sgi[k] < a.nseg;
+    const bool ok = live && has[k];
 #pragma unroll
     for (u32 q = 0; q < NSP; q++) {
       if (ok) {
-        const TreeSeg& sg = a.seg[sgi[k]];
-        span_any(sg.fm, sg.W + (u64)row[k] * sg.rb, c0 + 32 * q, wr[k] + 32 * q);
+        if (fm[k] == FM_F32) {
+          const float4* p = (const float4*)(wp[k] + 4 * (c0 + 32 * q));
+#pragma unroll
+          for (u32 g = 0; g < 8; g++) *(float4*)(wr[k] + 32 * q + 4 * g) = p[g];
+        } else {
+          span_any(fm[k], wp[k], c0 + 32 * q, wr[k] + 32 * q);
+        }
       } else {
 #pragma unroll
         for (u32 i = 0; i < 32; i++) wr[k][32 * q + i] = 0.0f;
       }
     }
   }
-  __syncthreads();
-  for (u32 tt = 0; tt < TT && t0 + tt < a.T; tt++) {
-    float4 xv[NQ];
+  float4 xl[16];
+  tree_mt_load_x<NSP, TT>(a, tid, tb, xl);
+  for (u32 j = 0; j < ntb; j++) {
+    const u32 t0 = tb + j * TT;
+    if (t0 >= a.T) break;  // block-uniform
+    if (j) __syncthreads();  // every wave is done with the previous tile's x
 #pragma unroll
-    for (u32 q = 0; q < NQ; q++) xv[q] = *(const float4*)(xsh + tt * 64 * LS + L * LS + 4 * q);
+    for (u32 jj = 0; jj < 16; jj++) {
+      const u32 i = tid + 256 * jj, tt = i / (64 * NQ), li = i % (64 * NQ);
+      xsh4[tt * 64 * LS4 + (li / NQ) * LS4 + li % NQ] = xl[jj];
+    }
+    __syncthreads();
+    if (j + 1 < ntb && t0 + TT < a.T) tree_mt_load_x<NSP, TT>(a, tid, t0 + TT, xl);  // next tile in flight
+    for (u32 tt = 0; tt < TT && t0 + tt < a.T; tt++) {
+      float4 xv[NQ];
 #pragma unroll
-    for (u32 k = 0; k < 2; k++) {
-      if (sgi[k] >= a.nseg) continue;
-      float n[NQ];
+      for (u32 q = 0; q < NQ; q++) xv[q] = xsh4[tt * 64 * LS4 + L * LS4 + q];
 #pragma unroll
-      for (u32 q = 0; q < NQ; q++) n[q] = leaf4(wr[k] + 4 * q, xv[q]);
-      const float v = tree64_asc(live ? tree_in_lane<NQ>(n) : 0.0f);  // a dead lane's leaves are +0 pads
-      const TreeSeg& sg = a.seg[sgi[k]];
-      if (L == 0) sg.out[(u64)(t0 + tt) * sg.ostride + row[k]] = sg.bias ? v + sg.bias[row[k]] : v;
+      for (u32 k = 0; k < 2; k++) {
+        if (!has[k]) continue;
+        float n[NQ];
+#pragma unroll
+        for (u32 q = 0; q < NQ; q++) n[q] = leaf4(wr[k] + 4 * q, xv[q]);
+        const float v = tree64_asc(live ? tree_in_lane<NQ>(n) : 0.0f);  // a dead lane's leaves are +0 pads
+        if (L == 0) op[k][(u64)(t0 + tt) * ost[k]] = hb[k] ? v + bia[k] : v;
+      }
     }
   }
 }
@@ -973,14 +1004,18 @@ int launch_tree_rows(const TreeArgs& a, u32 nsp, hipStream_t st) {
   if (a.T >= 16 && nsp <= 2) {  // token tiles: weights read once a tile
     const u32 tt = nsp == 1 ? 8u : 4u;
     const size_t sm = (size_t)tt * 64 * (32 * nsp + 4) * 4;
-    const dim3 grid((rows + 7) / 8, (a.T + tt - 1) / tt);
+    // tiles a block: about two blocks a CU over the whole grid, at least one tile each
+    const u32 rb = (rows + 7) / 8, nt = (a.T + tt - 1) / tt;
+    u32 ntb = rb * nt / 512;
+    ntb = ntb < 1 ? 1 : ntb > nt ? nt : ntb;
+    const dim3 grid(rb, (nt + ntb - 1) / ntb);
     static bool set1 = false, set2 = false;
     if (nsp == 1) {
       if (!set1) { (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<1, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm); set1 = true; }
-      LAUNCH_K((k_tree_rows_mt<1, 8>), grid, dim3(256), sm, st, a);
+      LAUNCH_K((k_tree_rows_mt<1, 8>), grid, dim3(256), sm, st, a, ntb);
     } else {
       if (!set2) { (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<2, 4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm); set2 = true; }
-      LAUNCH_K((k_tree_rows_mt<2, 4>), grid, dim3(256), sm, st, a);
+      LAUNCH_K((k_tree_rows_mt<2, 4>), grid, dim3(256), sm, st, a, ntb);
     }
     return 0;
   }
