@@ -44,10 +44,10 @@ TRAFFIC_KERNELS = {
     "k_tree_rows<": ("c2_decode", "route"),
     "k_gu_topk<": ("c2_decode", "gate_up"),
     "k_dn_lane<": ("c2_decode", "down"),
-    "k_moe_gemm2<1u, 0u>": ("c1_prefill_2048", "gate_up"),
-    "k_moe_gemm2<1u, 1u>": ("c1_prefill_2048", "down"),
-    "k_moe_gemm2<3u, 0u>": ("c1k_prefill_2048", "gate_up"),
-    "k_moe_gemm2<4u, 1u>": ("c1k_prefill_2048", "down"),
+    "k_moe_gemm3<1u, 0u>": ("c1_prefill_2048", "gate_up"),
+    "k_moe_gemm3<1u, 1u>": ("c1_prefill_2048", "down"),
+    "k_moe_gemm3<3u, 0u>": ("c1k_prefill_2048", "gate_up"),
+    "k_moe_gemm3<4u, 1u>": ("c1k_prefill_2048", "down"),
 }
 
 
@@ -113,9 +113,12 @@ MFMA_F16_PEAK_TFS = 2500.0
 
 
 def prefill(dev, shape, T, layers, steps, warmup, name=""):
-    """T-token chunks through `layers` resident layers on the f16 MFMA tier: tokens/s, and the gate/up
-    GEMM's MFMA rate (algorithmic flops 2 T nk dm ef x 2 per launch over its HIP-event time)."""
+    """T-token chunks through `layers` resident layers on the f16 MFMA tier (stacks packed once,
+    outside the timer): tokens/s, and the gate/up GEMM's MFMA rate (algorithmic flops 2 T nk dm ef x 2
+    per launch over its HIP-event time)."""
     Ls = [em.Layer(dev, shape, seed=1, layer=100 + i) for i in range(layers)]
+    for L in Ls:
+        L.pack()
     run = em.Runner(dev, shape, T, tier=em.F16)
     run.gen_inputs(1)
     dev.sync()
@@ -154,6 +157,9 @@ def prefill(dev, shape, T, layers, steps, warmup, name=""):
 def batched(dev, shape, T, layers, steps, warmup, tier):
     """config 3: T tokens a step through `layers` layers with the Zipf(1.1) router bias"""
     Ls = [em.Layer(dev, shape, seed=3, layer=200 + i, bias=em.zipf_bias(shape.ne, 3 + i)) for i in range(layers)]
+    if tier == em.F16:
+        for L in Ls:
+            L.pack()
     run = em.Runner(dev, shape, T, tier=tier)
     run.gen_inputs(3)
     for _ in range(warmup):
@@ -331,17 +337,17 @@ def main():
     if "prefill" in legs:
         pshape = em.SHAPES[args.prefill_config]
         out["prefill"] = prefill(dev, pshape, args.prefill_T, 4, max(2, args.steps // 4), 1, args.prefill_config)
-        out["prefill"]["config"] = f"{args.prefill_config} layer, {args.prefill_T}-token chunk, f16 MFMA tier"
+        out["prefill"]["config"] = f"{args.prefill_config} layer, {args.prefill_T}-token chunk, f16 MFMA tier, packed stacks"
     if "prefill_k" in legs:
         # the same layer shape with Q4_K gate / up and Q6_K down weight tiles
         out["prefill_k_quants"] = prefill(dev, em.SHAPES["c1k"], args.prefill_T, 4, max(2, args.steps // 4), 1, "c1k")
-        out["prefill_k_quants"]["config"] = f"c1k layer (Q4_K gate/up, Q6_K down), {args.prefill_T}-token chunk, f16 MFMA tier"
+        out["prefill_k_quants"]["config"] = f"c1k layer (Q4_K gate/up, Q6_K down), {args.prefill_T}-token chunk, f16 MFMA tier, packed stacks"
     if "c5" in legs:
         # config 5: one decode token and a 512-token chunk in one launch, Zipf(1.1) routing, 48 resident
         # layers (512 experts, top-10, ~1 GB each) cycled layer by layer
         c5 = batched(dev, em.SHAPES["c5"], 513, 48, 2, 1, em.F16)
         c5["tokens_per_s"] = round(513 / (c5["us_per_layer"] * 1e-6), 1)
-        c5["config"] = "c5: 48 layers x 512 experts top-10 (Q4_K gate/up, Q6_K down, shared expert), 1 + 512 tokens a launch, f16 tier"
+        c5["config"] = "c5: 48 layers x 512 experts top-10 (Q4_K gate/up, Q6_K down, shared expert), 1 + 512 tokens a launch, f16 tier, packed stacks"
         out["c5_mixed"] = c5
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(shape)

@@ -337,8 +337,8 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
   const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
   if (fg != fu) return fail(LLB_HIP_EINVAL, "f16 tier: gate and up in one format");
   if (L->sf && L->fsg != L->fsu) return fail(LLB_HIP_EINVAL, "f16 tier: shared gate and up in one format");
-  if (L->dm % 128 || L->ef % 128 || L->sf % 128 || L->ne >= 65536)
-    return fail(LLB_HIP_EINVAL, "f16 tier: dm, ef, sf multiples of 128");
+  if (L->dm % 256 || L->ef % 128 || L->sf % 128 || L->ne >= 65536)
+    return fail(LLB_HIP_EINVAL, "f16 tier: dm a multiple of 256, ef and sf of 128");
   const GemmScratch gs = gemm_layout(L, T);
   uint8_t* gb = sc + s.total;
   int rc;
@@ -371,6 +371,11 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
   g.tiles = tiles;
   g.ntiles = ntiles;
   g.out = gb + gs.act;
+  if (L->PG && L->PU) {
+    g.P0 = dp<uint8_t>(L->PG);
+    g.P1 = dp<uint8_t>(L->PU);
+    g.pes = pack_bytes(fg, L->ef, L->dm);
+  }
   stage_begin(ST_GU);
   if ((rc = launched(launch_moe_gemm(g, fg, 0, maxt, g_stream), "expert gate/up GEMM"))) return rc;
   stage_end(ST_GU);
@@ -385,6 +390,9 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
   d.arows = n;
   d.xmap = nullptr;
   d.out = gb + gs.out;
+  d.P0 = L->PD ? dp<uint8_t>(L->PD) : nullptr;
+  d.P1 = nullptr;
+  d.pes = pack_bytes(fd, L->dm, L->ef);
   stage_begin(ST_DN);
   if ((rc = launched(launch_moe_gemm(d, fd, 1, maxt, g_stream), "expert down GEMM"))) return rc;
   stage_end(ST_DN);
@@ -401,6 +409,10 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
     sg.A = x16;
     sg.arows = T;
     sg.out = gb + gs.sact;
+    if (L->PSG && L->PSU) {
+      sg.P0 = dp<uint8_t>(L->PSG);
+      sg.P1 = dp<uint8_t>(L->PSU);
+    }
     if ((rc = launched(launch_moe_gemm(sg, L->fsg, 0, mt, g_stream), "shared gate/up GEMM"))) return rc;
     GemmArgs sd{};
     sd.W0 = dp<uint8_t>(L->SD);
@@ -411,12 +423,71 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
     sd.A = (const _Float16*)(gb + gs.sact);
     sd.arows = T;
     sd.out = gb + gs.shd;
+    sd.P0 = L->PSD ? dp<uint8_t>(L->PSD) : nullptr;
     if ((rc = launched(launch_moe_gemm(sd, L->fsd, 1, mt, g_stream), "shared down GEMM"))) return rc;
     shd = (const float*)(gb + gs.shd);
   }
   return launched(launch_combine((const float*)(gb + gs.out), inv, wt, L->nk, shd, (const float*)(sc + s.sgo), x1, y,
                                  L->dm, T, g_stream),
                   "combine");
+}
+
+// packed stacks: G, U, D, then SG, SU, SD, each at a 256-byte boundary
+static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+struct PackPlan {
+  uint32_t fm[6], R[6], K[6], ne[6];
+  llb_dptr W[6];
+  uint64_t es[6];
+  size_t off[6], bytes;
+};
+static bool pack_plan(const llb_moe_layer* L, PackPlan& p) {
+  const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
+  if (fg != fu || L->dm % 256 || L->ef % 128 || L->sf % 128 || (L->sf && L->fsg != L->fsu)) return false;
+  const uint64_t rbg = row_bytes(fg, L->dm);
+  const uint32_t fm[6] = {fg, fu, fd, L->fsg, L->fsu, L->fsd};
+  const uint32_t R[6] = {L->ef, L->ef, L->dm, L->sf, L->sf, L->dm}, K[6] = {L->dm, L->dm, L->ef, L->dm, L->dm, L->sf};
+  const llb_dptr W[6] = {L->G, fz ? L->G + L->ef * rbg : L->U, L->D, L->SG, L->SU, L->SD};
+  p.bytes = 0;
+  for (int i = 0; i < 6; i++) {
+    const bool sh = i >= 3;
+    p.fm[i] = fm[i];
+    p.R[i] = R[i];
+    p.K[i] = K[i];
+    p.ne[i] = sh ? (L->sf ? 1 : 0) : L->ne;
+    p.W[i] = W[i];
+    p.es[i] = (uint64_t)(i < 2 && fz ? 2 : 1) * R[i] * row_bytes(fm[i], K[i]);
+    p.off[i] = p.bytes;
+    if (!p.ne[i]) continue;
+    const uint64_t b = pack_bytes(fm[i], R[i], K[i]);
+    if (!b) return false;
+    p.bytes = al256(p.bytes + b * p.ne[i]);
+  }
+  return true;
+}
+size_t llb_moe_hip_pack_bytes(const llb_moe_layer* L) {
+  PackPlan p;
+  return L && pack_plan(L, p) ? p.bytes : 0;
+}
+int llb_moe_hip_pack(llb_moe_layer* L, llb_dptr buf, size_t bytes) {
+  PackPlan p;
+  if (!L || !buf) return fail(LLB_HIP_EINVAL, "pack: null layer or buffer");
+  if (!pack_plan(L, p)) return fail(LLB_HIP_EINVAL, "pack: the f16 tier cannot take this layer");
+  if (bytes < p.bytes) return fail(LLB_HIP_EINVAL, "pack: buffer smaller than llb_moe_hip_pack_bytes");
+  int rc;
+  for (int i = 0; i < 6; i++) {
+    if (!p.ne[i]) continue;
+    if ((rc = launched(launch_pack(p.fm[i], dp<uint8_t>(p.W[i]), p.es[i], row_bytes(p.fm[i], p.K[i]), p.R[i], p.K[i],
+                                   p.ne[i], dp<uint8_t>(buf + p.off[i]), g_stream),
+                       "pack")))
+      return rc;
+  }
+  L->PG = buf + p.off[0];
+  L->PU = buf + p.off[1];
+  L->PD = buf + p.off[2];
+  L->PSG = L->sf ? buf + p.off[3] : 0;
+  L->PSU = L->sf ? buf + p.off[4] : 0;
+  L->PSD = L->sf ? buf + p.off[5] : 0;
+  return 0;
 }
 
 // the fused one-launch layer (exact tier, small T) on by default; 0 forces the four-launch path

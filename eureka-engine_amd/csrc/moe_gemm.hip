@@ -1,8 +1,8 @@
 // moe_gemm.hip -- the grouped-GEMM tier for many tokens (prefill, large batches): the expert products
 // on CDNA4 MFMA (v_mfma_f32_32x32x16_f16, f32 accumulate). The reference's fast prefill
 // (host/llb_pf.h:286-389, pfx_* on int8 mma.sync) groups slots by expert and runs one GEMM per
-// expert over its slots; so does this. Weight tiles are dequantized with the exact tier's decoders
-// (a 32-column span at a time) and rounded to f16 into LDS; activations are f16. Tolerance class.
+// expert over its slots; so does this. Weights are dequantized with the exact tier's decoders (a
+// 32-column span at a time) and rounded to f16 in registers; activations are f16. Tolerance class.
 //
 // Per expert e (slots off[e] .. off[e+1], rows of the slot-ordered activations):
 //   gate / up   act[s][n] = silu(G_e[n] . x_s) (U_e[n] . x_s), x_s = h2 of token xmap[s]
@@ -17,7 +17,10 @@
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-#define GM_BM 256  // slots a tile (an expert's slots split into tiles of this many)
+#define G3_MF 5                // 32-row fragments a tile
+#define GM_BM (32 * G3_MF)     // slots a tile (an expert's slots split into tiles of this many)
+#define G3_BM GM_BM
+
 
 // f32 rows -> f16 rows (the activations' one conversion)
 __global__ void __launch_bounds__(256) k_to_f16(const float* __restrict__ x, _Float16* __restrict__ y, u64 n) {
@@ -54,23 +57,347 @@ __global__ void __launch_bounds__(1024) k_tiles(const u32* __restrict__ off, u32
   if (t == 1023) *ntiles = part[1023];
 }
 
-// ---- the grouped GEMM. Block tile: BM = 256 slots x 128 weight rows (mode 0: 64 gate + 64 up
-// features, mode 1: 128 features), K in steps of 64, eight waves of 64 x 64 (2 x 2 MFMA 32x32x16
-// tiles; in mode 0 one wave's gate and up tiles cover the same 32 features, so the SwiGLU epilogue
-// pairs them in registers). A tile of 256 slots holds a whole expert at prefill sizes, so each weight
-// tile is read once. LDS holds two stages of A and B (f16, rows padded to 72 halves): while the
-// MFMAs run on one stage, the next three tiles' A rows and raw weight half-spans are in flight into
-// registers; after the MFMAs one tile is dequantized into the other stage. One barrier a k-tile.
-#define G2_BK 64
-#define G2_LD 72
-#define G2_BN 128                                  // weight rows a tile
-#define G2_STAGE ((GM_BM + G2_BN) * G2_LD)         // halves: A [256][72] then B [128][72]
+// ---- packed weights: a matrix of R rows x K columns re-laid in tiles of 32 rows x 64 columns, tile
+// (g, t) = rows 32 g .. 32 g + 31, columns 64 t .. 64 t + 63 at byte (g K / 64 + t) PK_TB<F>. In a
+// tile, lane l = 32 h + r owns row r, columns 32 h .. 32 h + 31: exactly the GEMM's B operand for a
+// k-tile, so a wave reads a tile with a few fully coalesced loads (planes of 64 lanes x 16 bytes)
+// instead of 64 scattered rows. The contents are the codes and f16 scales half_f16 derives from the
+// GGUF blocks (bit for bit the same weights):
+//   Q8_0  planes 0, 1: the codes of columns 0..15, 16..31 (q bytes); then 64 x u16 d
+//   Q4_K  plane 0: byte b = code b | code b + 16 << 4; then 64 x u32 {f16 d sc, f16 -dmin m}
+//   Q5_K  planes 0, 1: code bytes; then 64 x u32 {f16 d sc, f16 -dmin m}
+//   Q6_K  plane 0: low nibbles as Q4_K; then 64 x u64 {H0, H1}: bits 2 k, 2 k + 1 of byte i of Hj
+//         are the high two bits of code 16 j + 4 k + i; then 64 x u32 {f16 d sc0, f16 d sc1}
+template <u32 F> struct PK;
+template <> struct PK<FM_Q8_0> { static constexpr u32 TB = 2176; };
+template <> struct PK<FM_Q4_K> { static constexpr u32 TB = 1280; };
+template <> struct PK<FM_Q5_K> { static constexpr u32 TB = 2304; };
+template <> struct PK<FM_Q6_K> { static constexpr u32 TB = 1792; };
 
-// XCD-aware order: the hardware deals block b to XCD b % 8, so block b takes m-tile
-// 8 ((b / 8) / NT) + b % 8 and feature tile (b / 8) % NT: an m-tile's NT feature tiles all run on
-// one XCD and read its activation rows from that XCD's L2 (1-D grid, 8 NT ceil(tiles / 8) blocks)
-template <u32 F, u32 MODE>
-__global__ void __launch_bounds__(512) k_moe_gemm2(GemmArgs g, u32 NT) {
+// the codes half_f16 builds for half jh (byte 4 k + i of v[k] = code of column 16 jh + 4 k + i) and
+// its f16 scale pair {scale, min} as u32 (min 0 where the format has none)
+template <u32 F> DEV void half_codes(const Half<F>& h, u32 c0, u32 jh, u32* v, u32& s);
+template <> DEV void half_codes<FM_Q8_0>(const Half<FM_Q8_0>& h, u32, u32, u32* v, u32& s) {
+  v[0] = h.q.x; v[1] = h.q.y; v[2] = h.q.z; v[3] = h.q.w;
+  s = h.d & 0xffffu;
+}
+template <> DEV void half_codes<FM_Q4_K>(const Half<FM_Q4_K>& h, u32 c0, u32, u32* v, u32& s) {
+  const u32 j = (c0 & 255u) >> 5;
+  u32 sc, mn;
+  k4_scmin(h.h, j, sc, mn);
+  const h2v d1 = h2s(f16v(h.h.x & 0xffffu) * (float)sc), m1 = h2s(-(f16v(h.h.x >> 16) * (float)mn));
+  s = (as_u(d1) & 0xffffu) | (as_u(m1) << 16);
+  const u32 sh = 4u * (j & 1u);
+  const u32 q[4] = {h.q.x, h.q.y, h.q.z, h.q.w};
+#pragma unroll
+  for (int k = 0; k < 4; k++) v[k] = (q[k] >> sh) & 0x0F0F0F0Fu;
+}
+template <> DEV void half_codes<FM_Q5_K>(const Half<FM_Q5_K>& h, u32 c0, u32, u32* v, u32& s) {
+  const u32 j = (c0 & 255u) >> 5;
+  u32 sc, mn;
+  k4_scmin(h.h, j, sc, mn);
+  const h2v d1 = h2s(f16v(h.h.x & 0xffffu) * (float)sc), m1 = h2s(-(f16v(h.h.x >> 16) * (float)mn));
+  s = (as_u(d1) & 0xffffu) | (as_u(m1) << 16);
+  const u32 sh = 4u * (j & 1u);
+  const u32 q[4] = {h.q.x, h.q.y, h.q.z, h.q.w}, hh[4] = {h.qh.x, h.qh.y, h.qh.z, h.qh.w};
+#pragma unroll
+  for (int k = 0; k < 4; k++) v[k] = ((q[k] >> sh) & 0x0F0F0F0Fu) | (((hh[k] >> j) & 0x01010101u) << 4);
+}
+template <> DEV void half_codes<FM_Q6_K>(const Half<FM_Q6_K>& h, u32 c0, u32, u32* v, u32& s) {
+  const u32 r = c0 & 255u, quad = (r & 127u) >> 5;
+  const h2v ds = h2s(f16v(h.d) * (float)(int)(signed char)h.sc);
+  s = as_u(ds) & 0xffffu;
+  const u32 nsh = quad >= 2u ? 4u : 0u, hsh = 2u * quad;
+  const u32 l4[4] = {h.ql.x, h.ql.y, h.ql.z, h.ql.w}, h4[4] = {h.qh.x, h.qh.y, h.qh.z, h.qh.w};
+#pragma unroll
+  for (int k = 0; k < 4; k++) v[k] = ((l4[k] >> nsh) & 0x0F0F0F0Fu) | (((h4[k] >> hsh) & 0x03030303u) << 4);
+}
+
+// one wave a tile: grid (tiles of one matrix, ne), tiles = R / 32 * K / 64. W: GGUF rows (expert
+// stride es), P: packed (expert stride R / 32 * K / 64 * TB)
+template <u32 F>
+__global__ void __launch_bounds__(64) k_pack(const u8* __restrict__ W, u64 es, u64 rb, u32 K, u8* __restrict__ P) {
+  const u32 nkt = K / 64, tix = blockIdx.x, g = tix / nkt, t = tix % nkt, l = threadIdx.x, h = l >> 5, r = l & 31;
+  const u8* row = W + (u64)blockIdx.y * es + (u64)(32 * g + r) * rb;
+  u8* T = P + ((u64)blockIdx.y * gridDim.x + tix) * PK<F>::TB;
+  const u32 c0 = 64 * t + 32 * h;
+  Half<F> h0, h1;
+  h0.ld(row, c0, 0);
+  h1.ld(row, c0, 1);
+  u32 v0[4], v1[4], s0, s1;
+  half_codes<F>(h0, c0, 0, v0, s0);
+  half_codes<F>(h1, c0, 1, v1, s1);
+  if constexpr (F == FM_Q8_0 || F == FM_Q5_K) {
+    *(uint4*)(T + 16 * l) = make_uint4(v0[0], v0[1], v0[2], v0[3]);
+    *(uint4*)(T + 1024 + 16 * l) = make_uint4(v1[0], v1[1], v1[2], v1[3]);
+    if constexpr (F == FM_Q8_0) *(unsigned short*)(T + 2048 + 2 * l) = (unsigned short)s0;
+    else *(u32*)(T + 2048 + 4 * l) = s0;
+  } else {
+    u32 n[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) n[k] = (v0[k] & 0x0F0F0F0Fu) | ((v1[k] & 0x0F0F0F0Fu) << 4);
+    *(uint4*)(T + 16 * l) = make_uint4(n[0], n[1], n[2], n[3]);
+    if constexpr (F == FM_Q4_K) {
+      *(u32*)(T + 1024 + 4 * l) = s0;
+    } else {
+      u32 H0 = 0, H1 = 0;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        H0 |= ((v0[k] >> 4) & 0x03030303u) << (2 * k);
+        H1 |= ((v1[k] >> 4) & 0x03030303u) << (2 * k);
+      }
+      *(uint2*)(T + 1024 + 8 * l) = make_uint2(H0, H1);
+      *(u32*)(T + 1536 + 4 * l) = (s0 & 0xffffu) | (s1 << 16);
+    }
+  }
+}
+
+// a lane's share of one packed tile: ld issues the loads, f16(jh, o) gives the same eight u32 (16
+// halves, columns 16 jh .. 16 jh + 15 of the lane's span) as half_f16 on the GGUF blocks
+template <u32 F> struct PkB;
+template <> struct PkB<FM_Q8_0> {
+  uint4 q0, q1;
+  u32 d;
+  MDEV void ld(const u8* T, u32 l) {
+    q0 = *(const uint4*)(T + 16 * l);
+    q1 = *(const uint4*)(T + 1024 + 16 * l);
+    d = *(const unsigned short*)(T + 2048 + 2 * l);
+  }
+  MDEV void f16(u32 jh, u32* o) const {
+    const h2v dd = as_h2(d * 0x10001u), bias = h2s(1152.0f);
+    const uint4 q = jh ? q1 : q0;
+    const u32 qq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const u32 u = qq[k] ^ 0x80808080u;
+      o[2 * k] = as_u((mag_lo(u) - bias) * dd);
+      o[2 * k + 1] = as_u((mag_hi(u) - bias) * dd);
+    }
+  }
+};
+template <> struct PkB<FM_Q4_K> {
+  uint4 n;
+  u32 s;
+  MDEV void ld(const u8* T, u32 l) {
+    n = *(const uint4*)(T + 16 * l);
+    s = *(const u32*)(T + 1024 + 4 * l);
+  }
+  MDEV void f16(u32 jh, u32* o) const {
+    const h2v d1 = as_h2((s & 0xffffu) * 0x10001u), m1 = as_h2((s >> 16) * 0x10001u), bias = h2s(1024.0f);
+    const u32 nn[4] = {n.x, n.y, n.z, n.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const u32 v = (nn[k] >> (4 * jh)) & 0x0F0F0F0Fu;
+      o[2 * k] = as_u(__builtin_elementwise_fma(mag_lo(v) - bias, d1, m1));
+      o[2 * k + 1] = as_u(__builtin_elementwise_fma(mag_hi(v) - bias, d1, m1));
+    }
+  }
+};
+template <> struct PkB<FM_Q5_K> {
+  uint4 c0, c1;
+  u32 s;
+  MDEV void ld(const u8* T, u32 l) {
+    c0 = *(const uint4*)(T + 16 * l);
+    c1 = *(const uint4*)(T + 1024 + 16 * l);
+    s = *(const u32*)(T + 2048 + 4 * l);
+  }
+  MDEV void f16(u32 jh, u32* o) const {
+    const h2v d1 = as_h2((s & 0xffffu) * 0x10001u), m1 = as_h2((s >> 16) * 0x10001u), bias = h2s(1024.0f);
+    const uint4 c = jh ? c1 : c0;
+    const u32 cc[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      o[2 * k] = as_u(__builtin_elementwise_fma(mag_lo(cc[k]) - bias, d1, m1));
+      o[2 * k + 1] = as_u(__builtin_elementwise_fma(mag_hi(cc[k]) - bias, d1, m1));
+    }
+  }
+};
+template <> struct PkB<FM_Q6_K> {
+  uint4 n;
+  uint2 H;
+  u32 s;
+  MDEV void ld(const u8* T, u32 l) {
+    n = *(const uint4*)(T + 16 * l);
+    H = *(const uint2*)(T + 1024 + 8 * l);
+    s = *(const u32*)(T + 1536 + 4 * l);
+  }
+  MDEV void f16(u32 jh, u32* o) const {
+    const h2v ds = as_h2((jh ? s >> 16 : s & 0xffffu) * 0x10001u), bias = h2s(1056.0f);
+    const u32 hh = jh ? H.y : H.x;
+    const u32 nn[4] = {n.x, n.y, n.z, n.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const u32 v = ((nn[k] >> (4 * jh)) & 0x0F0F0F0Fu) | (((hh >> (2 * k)) & 0x03030303u) << 4);
+      o[2 * k] = as_u((mag_lo(v) - bias) * ds);
+      o[2 * k + 1] = as_u((mag_hi(v) - bias) * ds);
+    }
+  }
+};
+
+// a lane's weights of one k-tile for one of its rows: from the GGUF row (base = the row) or from the
+// packed tiles (base = the row group's tile 0); f16(jh, o) = half_f16 of half jh of the span
+template <u32 F, bool PKD> struct BRow;
+template <u32 F> struct BRow<F, false> {
+  Half<F> a, b;
+  u32 c0;
+  MDEV void ld(const u8* base, u32 t, u32 l) {
+    c0 = 64 * t + 32 * (l >> 5);
+    a.ld(base, c0, 0);
+    b.ld(base, c0, 1);
+  }
+  MDEV void f16(u32 jh, u32* o) const { half_f16<F>(jh ? b : a, c0, jh, o); }
+};
+template <u32 F> struct BRow<F, true> {
+  PkB<F> p;
+  MDEV void ld(const u8* base, u32 t, u32 l) { p.ld(base + (u64)t * PK<F>::TB, l); }
+  MDEV void f16(u32 jh, u32* o) const { p.f16(jh, o); }
+};
+
+// ---- the grouped GEMM, weights in registers. Block: 4 waves, a tile of up to G3_BM = 160 slots
+// (five 32-row fragments) x 256 weight rows (mode 0: 128 gate + 128 up features, mode 1: 256
+// features); wave w owns 64 weight rows (mode 0: gate and up rows of features 32 w .. 32 w + 31, so
+// the SwiGLU epilogue pairs them in registers) for every slot of the tile. Each lane dequantizes its
+// own weight rows straight into the MFMA B operand: within a k-tile of 64 columns the K order is
+// permuted (MFMA k-slot 8 h + e of step s is column 32 h + 8 s + e, lane half h = lane / 32, for A
+// and B alike), so a lane's columns for the whole k-tile are one 32-column quant span, decoded once.
+// Only the activations go through LDS (two stages of 160 rows x 64 halves, padded to 72), read by
+// all four waves. The number of live fragments NL = ceil(rows / 32) is a compile-time variant, so
+// dead rows cost neither loads nor MFMAs. Three register slots rotate: at k-tile t a slot's weights
+// are decoded and multiplied, the next tile's activations are stored, and the slot is refilled with
+// tile t + 3; one barrier a k-tile.
+#define G3_BK 64  // columns a k-tile
+#define G3_LD 72
+#define G3_STAGE (G3_BM * G3_LD)  // halves
+
+template <u32 F, u32 MODE, bool PKD, u32 NL>
+DEV void gemm3_body(const GemmArgs& g, _Float16* lds, u32 e, u32 base, u32 m0, u32 M, u32 ntile) {
+  const u32 tid = threadIdx.x, w = tid >> 6, l = tid & 63, h = l >> 5, lr = l & 31;
+  // A: chunk i of a thread is row 32 i + tid / 8, 16-byte chunk tid % 8 of the k-tile; rows past the
+  // tile's slots get an offset past the buffer bound (zeros, no access), so loads stay unconditional
+  const __amdgpu_buffer_rsrc_t arsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)g.A, (short)0, (int)(g.arows * g.K * 2u), 0x00020000);
+  u32 aoff[NL], src[NL];
+#pragma unroll
+  for (u32 i = 0; i < NL; i++) src[i] = base + m0 + min(32 * i + (tid >> 3), M - m0 - 1);  // a live slot
+  if (MODE == 0 && g.xmap) {
+#pragma unroll
+    for (u32 i = 0; i < NL; i++) src[i] = g.xmap[src[i]];
+  }
+#pragma unroll
+  for (u32 i = 0; i < NL; i++)
+    aoff[i] = m0 + 32 * i + (tid >> 3) < M ? (src[i] * g.K + 8 * (tid & 7)) * 2u : 0x80000000u;
+  const u32 nk = g.K / G3_BK;
+  // B: this lane's two weight rows (GGUF rows, or their row groups' packed tiles)
+  const u8 *br0, *br1;
+  if constexpr (PKD) {
+    const u64 g0 = MODE == 0 ? 4 * ntile + w : 8 * ntile + 2 * w, tb = (u64)nk * PK<F>::TB;
+    br0 = g.P0 + (u64)e * g.pes + g0 * tb;
+    br1 = MODE == 0 ? g.P1 + (u64)e * g.pes + g0 * tb : br0 + tb;
+  } else if (MODE == 0) {
+    const u64 f = (u64)ntile * 128 + 32 * w + lr;
+    br0 = g.W0 + (u64)e * g.es + f * g.rb;
+    br1 = g.W1 + (u64)e * g.es + f * g.rb;
+  } else {
+    const u64 n = (u64)ntile * 256 + 64 * w + lr;
+    br0 = g.W0 + (u64)e * g.es + n * g.rb;
+    br1 = br0 + 32 * g.rb;
+  }
+  struct Slot {
+    uint4 a[NL];
+    BRow<F, PKD> b0, b1;
+  };
+  Slot s0, s1, s2;
+  auto load = [&](Slot& s, u32 t) {
+    const u32 tc = min(t, nk - 1), k0 = tc * G3_BK;  // past the end: a repeat of the last tile, never used
+#pragma unroll
+    for (u32 i = 0; i < NL; i++) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(arsrc, (int)(aoff[i] + 2 * k0), 0, 0);
+      s.a[i] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+    s.b0.ld(br0, tc, l);
+    s.b1.ld(br1, tc, l);
+  };
+  auto store = [&](const Slot& s, u32 t) {
+    _Float16* As = lds + (t & 1) * G3_STAGE;
+#pragma unroll
+    for (u32 i = 0; i < NL; i++) *(uint4*)(As + (32 * i + (tid >> 3)) * G3_LD + 8 * (tid & 7)) = s.a[i];
+  };
+  f32x16 acc[NL][2];
+#pragma unroll
+  for (u32 a = 0; a < NL; a++)
+#pragma unroll
+    for (u32 b = 0; b < 2; b++)
+#pragma unroll
+      for (u32 i = 0; i < 16; i++) acc[a][b][i] = 0.0f;
+  // decode the slot's weights (step s of row b: halves o[4 (s % 2) ..] of half s / 2), multiply tile t
+  auto mma = [&](const Slot& s, u32 t) {
+    u32 o00[8], o01[8], o10[8], o11[8];
+    s.b0.f16(0, o00);
+    s.b0.f16(1, o01);
+    s.b1.f16(0, o10);
+    s.b1.f16(1, o11);
+    const _Float16* As = lds + (t & 1) * G3_STAGE + lr * G3_LD + 32 * h;
+#pragma unroll
+    for (u32 st = 0; st < 4; st++) {
+      const u32* p0 = st < 2 ? o00 : o01;
+      const u32* p1 = st < 2 ? o10 : o11;
+      const u32 j = 4 * (st & 1);
+      h8 b0, b1;
+      __builtin_memcpy(&b0, p0 + j, 16);
+      __builtin_memcpy(&b1, p1 + j, 16);
+#pragma unroll
+      for (u32 mf = 0; mf < NL; mf++) {
+        const h8 a = *(const h8*)(As + 32 * mf * G3_LD + 8 * st);
+        acc[mf][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b0, acc[mf][0], 0, 0, 0);
+        acc[mf][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b1, acc[mf][1], 0, 0, 0);
+      }
+    }
+  };
+  // k-tile t with slot X (holding tile t) and Y (tile t + 1): store Y's activations into the other
+  // stage, multiply X, refill X with tile t + 3
+  auto step = [&](Slot& X, const Slot& Y, u32 t) {
+    if (t + 1 < nk) store(Y, t + 1);
+    mma(X, t);
+    load(X, t + 3);
+    __syncthreads();
+  };
+  load(s0, 0);
+  load(s1, 1);
+  load(s2, 2);
+  store(s0, 0);
+  __syncthreads();
+  u32 t = 0;
+  for (; t + 3 <= nk; t += 3) {
+    step(s0, s1, t);
+    step(s1, s2, t + 1);
+    step(s2, s0, t + 2);
+  }
+  if (t < nk) step(s0, s1, t);  // nk % 3 tiles left
+  if (t + 1 < nk) step(s1, s2, t + 1);
+  // epilogue: acc[mf][b][i] is slot row 32 mf + 8 (i / 4) + 4 h + i % 4 of the tile, weight row lr
+  // of the wave's row block b
+#pragma unroll
+  for (u32 mf = 0; mf < NL; mf++)
+#pragma unroll
+    for (u32 i = 0; i < 16; i++) {
+      const u32 row = 32 * mf + 8 * (i >> 2) + 4 * h + (i & 3);
+      if (m0 + row >= M) continue;
+      const u64 s = base + m0 + row;
+      if (MODE == 0) {
+        const float gv = acc[mf][0][i], uv = acc[mf][1][i];
+        ((_Float16*)g.out)[s * g.N + ntile * 128 + 32 * w + lr] = (_Float16)(gv / (1.0f + __expf(-gv)) * uv);
+      } else {
+#pragma unroll
+        for (u32 b = 0; b < 2; b++) ((float*)g.out)[s * g.N + ntile * 256 + 64 * w + 32 * b + lr] = acc[mf][b][i];
+      }
+    }
+}
+
+// XCD-aware order: the hardware deals block b to XCD b % 8, so block b takes tile 8 ((b / 8) / NT) +
+// b % 8 and weight-row tile (b / 8) % NT: a tile's NT weight-row tiles all run on one XCD and read its
+// activation rows from that XCD's L2 (1-D grid, 8 NT ceil(tiles / 8) blocks)
+template <u32 F, u32 MODE, bool PKD>
+__global__ void __launch_bounds__(256) k_moe_gemm3(GemmArgs g, u32 NT) {
   extern __shared__ _Float16 lds[];
   const u32 bi = blockIdx.x >> 3, tile = 8 * (bi / NT) + (blockIdx.x & 7), ntile = bi % NT;
   u32 e, m0, base, M;
@@ -78,150 +405,24 @@ __global__ void __launch_bounds__(512) k_moe_gemm2(GemmArgs g, u32 NT) {
     if (tile >= *g.ntiles) return;
     const u32 tv = g.tiles[tile];
     e = tv >> 16;
-    m0 = (tv & 0xffffu) * GM_BM;
+    m0 = (tv & 0xffffu) * G3_BM;
     base = g.off[e];
     M = g.off[e + 1] - base;
   } else {
     e = 0;
-    m0 = tile * GM_BM;
+    m0 = tile * G3_BM;
     base = 0;
     M = g.M;
     if (m0 >= M) return;
   }
-  constexpr u32 NF = MODE == 0 ? 64u : 128u;  // output features a block
-  const u32 n0 = ntile * NF, tid = threadIdx.x, w = tid >> 6, l = tid & 63, wm = w >> 1, wn = w & 1;
-  // A: 256 rows x 64 halves a k-tile, 16-byte chunks c = tid + 512 i (i < 4): row c / 8, chunk c % 8.
-  // Buffer loads bounded by A's size: a row past the expert's slots gets an offset past the bound, so
-  // its load returns zeros without touching memory, and every load stays unconditional (a load under a
-  // branch makes the compiler wait for all of them)
-  const __amdgpu_buffer_rsrc_t arsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)g.A, (short)0, (int)(g.arows * g.K * 2u), 0x00020000);
-  u32 aoff[4], src[4];
-#pragma unroll
-  for (u32 i = 0; i < 4; i++) src[i] = base + m0 + min((tid + 512 * i) >> 3, M - m0 - 1);  // a live slot
-  if (MODE == 0 && g.xmap) {  // slot -> token row, the four reads in flight together
-#pragma unroll
-    for (u32 i = 0; i < 4; i++) src[i] = g.xmap[src[i]];
+  const u32 rows = min(M - m0, (u32)G3_BM);
+  switch ((rows + 31) / 32) {  // block-uniform
+    case 1: gemm3_body<F, MODE, PKD, 1>(g, lds, e, base, m0, M, ntile); break;
+    case 2: gemm3_body<F, MODE, PKD, 2>(g, lds, e, base, m0, M, ntile); break;
+    case 3: gemm3_body<F, MODE, PKD, 3>(g, lds, e, base, m0, M, ntile); break;
+    case 4: gemm3_body<F, MODE, PKD, 4>(g, lds, e, base, m0, M, ntile); break;
+    default: gemm3_body<F, MODE, PKD, 5>(g, lds, e, base, m0, M, ntile); break;
   }
-#pragma unroll
-  for (u32 i = 0; i < 4; i++) {
-    const u32 c = tid + 512 * i, r = c >> 3;
-    aoff[i] = m0 + r < M ? (src[i] * g.K + 8 * (c & 7)) * 2u : 0x80000000u;
-  }
-  // B: 128 rows x 64 columns a k-tile; thread: row tid / 4, span (tid / 2) % 2, half tid % 2
-  const u32 br = tid >> 2, bs = (tid >> 1) & 1, bj = tid & 1;
-  const u8* brow;
-  if (MODE == 0) brow = (br < 64 ? g.W0 + (u64)(n0 + br) * g.rb : g.W1 + (u64)(n0 + br - 64) * g.rb) + (u64)e * g.es;
-  else brow = g.W0 + (u64)e * g.es + (u64)(n0 + br) * g.rb;
-  // a wave whose 64 rows are all past the expert's slots skips its MFMAs (wave-uniform)
-  const bool live = m0 + 64 * wm < M;
-
-  // three register slots keep k-tiles t + 2 .. t + 4 in flight while tile t is multiplied (slot of
-  // tile u: u % 3); compile-time slot choice keeps them in registers
-  struct Slot {
-    uint4 a[4];
-    Half<F> h;
-  };
-  Slot s0, s1, s2;
-  const u32 nk = g.K / G2_BK;
-  auto load = [&](Slot& s, u32 t) {
-    const u32 k0 = min(t, nk - 1) * G2_BK;  // past the end: a repeat of the last tile, never stored
-#pragma unroll
-    for (u32 i = 0; i < 4; i++) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(arsrc, (int)(aoff[i] + 2 * k0), 0, 0);
-      s.a[i] = make_uint4(v[0], v[1], v[2], v[3]);
-    }
-    s.h.ld(brow, k0 + 32 * bs, bj);
-  };
-  auto store = [&](const Slot& s, u32 t) {
-    _Float16* As = lds + (t & 1) * G2_STAGE;
-    _Float16* Bs = As + GM_BM * G2_LD;
-    const u32 k0 = t * G2_BK;
-#pragma unroll
-    for (u32 i = 0; i < 4; i++) {
-      const u32 c = tid + 512 * i;
-      *(uint4*)(As + (c >> 3) * G2_LD + 8 * (c & 7)) = s.a[i];
-    }
-    u32 o[8];
-    half_f16<F>(s.h, k0 + 32 * bs, bj, o);
-    _Float16* d = Bs + br * G2_LD + 32 * bs + 16 * bj;
-    *(uint4*)d = make_uint4(o[0], o[1], o[2], o[3]);
-    *(uint4*)(d + 8) = make_uint4(o[4], o[5], o[6], o[7]);
-  };
-
-  f32x16 acc[2][2];
-#pragma unroll
-  for (u32 a = 0; a < 2; a++)
-#pragma unroll
-    for (u32 b = 0; b < 2; b++)
-#pragma unroll
-      for (u32 i = 0; i < 16; i++) acc[a][b][i] = 0.0f;
-  // B rows of this wave's two 32-column tiles
-  const u32 bro0 = MODE == 0 ? 32 * wn : 64 * wn, bro1 = MODE == 0 ? 64 + 32 * wn : 64 * wn + 32;
-  auto mma = [&](u32 t) {
-    if (!live) return;
-    const _Float16* As = lds + (t & 1) * G2_STAGE;
-    const _Float16* Bs = As + GM_BM * G2_LD;
-#pragma unroll
-    for (u32 ks = 0; ks < G2_BK / 16; ks++) {
-      const u32 ko = 16 * ks + 8 * (l >> 5);
-      const h8 a0 = *(const h8*)(As + (64 * wm + (l & 31)) * G2_LD + ko);
-      const h8 a1 = *(const h8*)(As + (64 * wm + 32 + (l & 31)) * G2_LD + ko);
-      const h8 b0 = *(const h8*)(Bs + (bro0 + (l & 31)) * G2_LD + ko);
-      const h8 b1 = *(const h8*)(Bs + (bro1 + (l & 31)) * G2_LD + ko);
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, acc[1][1], 0, 0, 0);
-    }
-  };
-  // iteration t: multiply tile t, store tile t + 1 (its slot) into the other stage, refill that
-  // slot with tile t + 4, one barrier. The steady-state loop runs while three tiles follow, so its
-  // stores and loads are unconditional; the last one to three iterations only multiply and store.
-  auto step = [&](Slot& s, u32 t) {
-    mma(t);
-    store(s, t + 1);
-    load(s, t + 4);
-    __syncthreads();
-  };
-  auto tail = [&](const Slot& s, u32 t) {
-    mma(t);
-    if (t + 1 < nk) store(s, t + 1);
-    __syncthreads();
-  };
-  load(s0, 0);
-  load(s1, 1);
-  load(s2, 2);
-  store(s0, 0);
-  load(s0, 3);
-  __syncthreads();
-  u32 t = 0;
-  for (; t + 4 <= nk; t += 3) {
-    step(s1, t);
-    step(s2, t + 1);
-    step(s0, t + 2);
-  }
-  // 1 .. 3 tiles left; their slots continue the rotation
-  tail(s1, t);
-  if (t + 1 < nk) tail(s2, t + 1);
-  if (t + 2 < nk) tail(s0, t + 2);
-  // epilogue: acc[a][b][i] is row 64 wm + 32 a + 8 (i / 4) + 4 (l / 32) + i % 4 of the tile,
-  // column l % 32 of B tile b
-#pragma unroll
-  for (u32 a = 0; a < 2; a++)
-#pragma unroll
-    for (u32 i = 0; i < 16; i++) {
-      const u32 row = 64 * wm + 32 * a + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
-      if (m0 + row >= M) continue;
-      const u64 s = base + m0 + row;
-      if (MODE == 0) {
-        const float gv = acc[a][0][i], uv = acc[a][1][i];
-        ((_Float16*)g.out)[s * g.N + n0 + 32 * wn + (l & 31)] = (_Float16)(gv / (1.0f + __expf(-gv)) * uv);
-      } else {
-#pragma unroll
-        for (u32 b = 0; b < 2; b++) ((float*)g.out)[s * g.N + n0 + 64 * wn + 32 * b + (l & 31)] = acc[a][b][i];
-      }
-    }
 }
 
 // y[t][r] = (sum_j, rank order, wt[t][j] out[inv[t nk + j]][r]) + sgo[t] shd[t][r] + x1[t][r]
@@ -272,29 +473,50 @@ __global__ void __launch_bounds__(256) k_combine(const float* __restrict__ out, 
 
 // ---------------------------------------------------------------- launchers
 
-template <u32 F, u32 MODE> static void gemm2_go(const GemmArgs& g, dim3 grid, size_t sm, hipStream_t st) {
+template <u32 F, u32 MODE, bool PKD> static void gemm3_go(const GemmArgs& g, dim3 grid, size_t sm, hipStream_t st) {
   static bool set = false;
   if (!set) {
-    (void)hipFuncSetAttribute((const void*)k_moe_gemm2<F, MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
+    (void)hipFuncSetAttribute((const void*)k_moe_gemm3<F, MODE, PKD>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
     set = true;
   }
-  LAUNCH_K((k_moe_gemm2<F, MODE>), grid, dim3(512), sm, st, g, g.N / (MODE == 0 ? 64u : 128u));
+  LAUNCH_K((k_moe_gemm3<F, MODE, PKD>), grid, dim3(256), sm, st, g, g.N / (MODE == 0 ? 128u : 256u));
 }
 
 int launch_moe_gemm(const GemmArgs& g, u32 fm, u32 mode, u32 grid_y, hipStream_t st) {
-  const u32 nf = mode == 0 ? 64u : 128u;
+  const u32 nf = mode == 0 ? 128u : 256u;
   // A's buffer loads take 32-bit offsets below 2^31 (dead rows use 2^31)
-  if (g.K % G2_BK || g.N % nf || fm == FM_F32 || (u64)g.arows * g.K * 2 >= (1ull << 31)) return -1;
+  if (g.K % G3_BK || g.N % nf || fm == FM_F32 || (u64)g.arows * g.K * 2 >= (1ull << 31)) return -1;
   const dim3 grid(8 * (g.N / nf) * ((grid_y + 7) / 8));
-  const size_t sm = (size_t)2 * G2_STAGE * 2;
-#define G2_L(F) \
+  const size_t sm = (size_t)2 * G3_STAGE * 2;
+  const bool pk = g.P0 != nullptr;
+#define G3_L(F) \
   if (fm == F) { \
-    if (mode == 0) gemm2_go<F, 0>(g, grid, sm, st); \
-    else gemm2_go<F, 1>(g, grid, sm, st); \
+    if (mode == 0) pk ? gemm3_go<F, 0, true>(g, grid, sm, st) : gemm3_go<F, 0, false>(g, grid, sm, st); \
+    else pk ? gemm3_go<F, 1, true>(g, grid, sm, st) : gemm3_go<F, 1, false>(g, grid, sm, st); \
     return 0; \
   }
-  G2_L(FM_Q8_0) G2_L(FM_Q4_K) G2_L(FM_Q6_K) G2_L(FM_Q5_K)
-#undef G2_L
+  G3_L(FM_Q8_0) G3_L(FM_Q4_K) G3_L(FM_Q6_K) G3_L(FM_Q5_K)
+#undef G3_L
+  return -1;
+}
+
+// packed copy of ne stacked matrices of R rows x K columns (GGUF expert stride es, row bytes rb)
+u64 pack_bytes(u32 fm, u32 R, u32 K) {
+  if (R % 32 || K % 64) return 0;
+  u32 tb = 0;
+  if (fm == FM_Q8_0) tb = PK<FM_Q8_0>::TB;
+  else if (fm == FM_Q4_K) tb = PK<FM_Q4_K>::TB;
+  else if (fm == FM_Q5_K) tb = PK<FM_Q5_K>::TB;
+  else if (fm == FM_Q6_K) tb = PK<FM_Q6_K>::TB;
+  return (u64)(R / 32) * (K / 64) * tb;
+}
+int launch_pack(u32 fm, const u8* W, u64 es, u64 rb, u32 R, u32 K, u32 ne, u8* P, hipStream_t st) {
+  if (!pack_bytes(fm, R, K) || ne == 0) return -1;
+  const dim3 grid((R / 32) * (K / 64), ne);
+#define PK_L(F) \
+  if (fm == F) { LAUNCH_K((k_pack<F>), grid, dim3(64), 0, st, W, es, rb, K, P); return 0; }
+  PK_L(FM_Q8_0) PK_L(FM_Q4_K) PK_L(FM_Q6_K) PK_L(FM_Q5_K)
+#undef PK_L
   return -1;
 }
 

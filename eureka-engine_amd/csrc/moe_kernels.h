@@ -118,9 +118,15 @@ struct GemmArgs {
   const uint32_t* tiles;  // tile list (e << 16 | tile), or null
   const uint32_t* ntiles;
   void* out;          // mode 0: f16 [slots][N]; mode 1: f32 [slots][N]
+  const uint8_t* P0;  // packed W0 (null: read the GGUF rows)
+  const uint8_t* P1;  // packed W1 (mode 0)
+  uint64_t pes;       // packed expert stride
 };
 int launch_moe_gemm(const GemmArgs& g, uint32_t fm, uint32_t mode, uint32_t grid_y, hipStream_t st);
 uint32_t gemm_bm();
+uint64_t pack_bytes(uint32_t fm, uint32_t R, uint32_t K);
+int launch_pack(uint32_t fm, const uint8_t* W, uint64_t es, uint64_t rb, uint32_t R, uint32_t K, uint32_t ne,
+                uint8_t* P, hipStream_t st);
 int launch_to_f16(const float* x, _Float16* y, uint64_t n, hipStream_t st);
 int launch_tiles(const uint32_t* off, uint32_t ne, uint32_t* tiles, uint32_t* ntiles, hipStream_t st);
 int launch_combine(const float* out, const uint32_t* inv, const float* wt, uint32_t nk, const float* shd,

@@ -38,7 +38,9 @@ class MoeLayer(C.Structure):
     _fields_ = [("dm", C.c_uint32), ("ne", C.c_uint32), ("nk", C.c_uint32), ("ef", C.c_uint32), ("sf", C.c_uint32),
                 ("fx", C.c_uint32), ("fsg", C.c_uint32), ("fsu", C.c_uint32), ("fsd", C.c_uint32), ("pad", C.c_uint32),
                 ("router", C.c_uint64), ("shgate", C.c_uint64), ("G", C.c_uint64), ("U", C.c_uint64), ("D", C.c_uint64),
-                ("SG", C.c_uint64), ("SU", C.c_uint64), ("SD", C.c_uint64), ("router_bias", C.c_uint64)]
+                ("SG", C.c_uint64), ("SU", C.c_uint64), ("SD", C.c_uint64), ("router_bias", C.c_uint64),
+                ("PG", C.c_uint64), ("PU", C.c_uint64), ("PD", C.c_uint64),
+                ("PSG", C.c_uint64), ("PSU", C.c_uint64), ("PSD", C.c_uint64)]
 
 
 _SIGS = {
@@ -67,6 +69,8 @@ _SIGS = {
     "llb_moe_hip_forward": (C.c_int, [C.POINTER(MoeLayer), C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64,
                                       C.c_uint64, C.c_uint64, C.c_size_t, C.c_int]),
     "llb_moe_hip_set_fused": (C.c_int, [C.c_int]),
+    "llb_moe_hip_pack_bytes": (C.c_size_t, [C.POINTER(MoeLayer)]),
+    "llb_moe_hip_pack": (C.c_int, [C.POINTER(MoeLayer), C.c_uint64, C.c_size_t]),
     "llb_moe_hip_status": (C.c_int, [C.c_uint64, C.POINTER(MoeLayer), C.c_uint32]),
     "llb_moe_hip_topk": (C.c_int, [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64,
                                    C.c_uint64, C.c_uint64]),
@@ -255,8 +259,28 @@ class Layer:
         self.desc = MoeLayer(s.dm, s.ne, s.nk, s.ef, s.sf, s.fx, s.fsg, s.fsu, s.fsd, 0, self.router, self.shgate,
                              self.G, self.U, self.D, self.SG, self.SU, self.SD, self.bias)
 
+        self.packed = 0
+
+    def pack(self):
+        """packed copies of the stacks for the f16 tier (llb_moe_hip_pack); returns the bytes used."""
+        n = self.dev.lib.llb_moe_hip_pack_bytes(C.byref(self.desc))
+        if not n:
+            raise LlbError("llb_moe_hip_pack_bytes: layer cannot be packed")
+        self.unpack()
+        self.packed = self.dev.alloc(n)
+        self.dev.check(self.dev.lib.llb_moe_hip_pack(C.byref(self.desc), self.packed, n))
+        return n
+
+    def unpack(self):
+        """drop the packed copies (the f16 tier reads the GGUF stacks again)."""
+        if self.packed:
+            self.dev.free(self.packed)
+        self.packed = 0
+        for f in ("PG", "PU", "PD", "PSG", "PSU", "PSD"):
+            setattr(self.desc, f, 0)
+
     def free(self):
-        for p in (self.router, self.shgate, self.G, self.U, self.D, self.SG, self.SU, self.SD, self.bias):
+        for p in (self.router, self.shgate, self.G, self.U, self.D, self.SG, self.SU, self.SD, self.bias, self.packed):
             if p:
                 self.dev.free(p)
 

@@ -81,6 +81,8 @@ typedef struct {
   llb_dptr SG, SU, SD; /* shared expert */
   llb_dptr router_bias; /* F32 [ne] added to each router logit, one rounding (0: none). Not in the
                          * reference: the batched-decode workload skews expert load with it */
+  llb_dptr PG, PU, PD;    /* packed copies of G, U, D for the f16 tier (llb_moe_hip_pack; 0: none) */
+  llb_dptr PSG, PSU, PSD; /* packed copies of SG, SU, SD */
 } llb_moe_layer;
 
 /* ---- the layer's table row (host code) ----
@@ -114,6 +116,16 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
  * launch on that scratch had a bounded wait time out. No counterpart in the reference. */
 int llb_moe_hip_set_fused(int on);
 int llb_moe_hip_status(llb_dptr scratch, const llb_moe_layer* L, uint32_t T);
+
+/* ---- packed weights for the f16 tier. No counterpart in the reference, whose prefill decodes GGUF
+ * blocks where they lie. The grouped GEMM reads each weight tile of 32 rows x 64 columns as one
+ * coalesced block when the stacks are re-laid once into tiles in its operand order; the packed copy
+ * holds the same codes and f16 scales the GEMM derives from the GGUF blocks, so results are the same
+ * bit for bit. pack_bytes: device bytes for packed copies of every stack of L (0 when the f16 tier
+ * cannot take L). pack: fills buf (at least pack_bytes) from L's GGUF stacks, on the library stream,
+ * and sets L->PG .. L->PSD; layers without them keep working on the GGUF stacks. */
+size_t llb_moe_hip_pack_bytes(const llb_moe_layer* L);
+int llb_moe_hip_pack(llb_moe_layer* L, llb_dptr buf, size_t bytes);
 
 /* ---- kernel-level entry points ---- */
 /* llb_moe_topk block 0 (tools/payload-moeany.patch:311-470) for T tokens: lg [T][lstride] (ne logits,

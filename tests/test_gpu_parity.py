@@ -336,6 +336,34 @@ def test_f16_tier_config5_mixed(dev):
     assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
 
 
+PACK_CASES = [(f"small{i}", i, 150) for i in range(len(SMALL))] + [("c1", None, 300), ("c1k", None, 300), ("c2", None, 40)]
+
+
+@pytest.mark.parametrize("name,si,T", PACK_CASES)
+def test_f16_packed_matches_gguf(dev, name, si, T):
+    """the f16 tier on packed stacks (llb_moe_hip_pack) gives the same bits as on the GGUF stacks, for
+    every weight format, the shared expert and ragged expert tiles; the packed bytes are the same after
+    packing twice"""
+    shape = SMALL[si] if si is not None else em.SHAPES[name]
+    _say("f16 packed vs gguf", name, "T", T)
+    layer = em.Layer(dev, shape, seed=9)
+    run = em.Runner(dev, shape, T, tier=em.F16)
+    run.gen_inputs(9)
+    run.forward(layer)
+    y0, ids0, wt0 = run.outputs()
+    n = layer.pack()
+    run.forward(layer)
+    y1, ids1, wt1 = run.outputs()
+    p1 = dev.read(layer.packed, (n,), np.uint8)
+    layer.pack()
+    p2 = dev.read(layer.packed, (n,), np.uint8)
+    run.free()
+    layer.free()
+    assert np.array_equal(ids0, ids1) and np.array_equal(wt0.view(np.uint32), wt1.view(np.uint32))
+    assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32)), np.abs(y0 - y1).max()
+    assert np.array_equal(p1, p2)
+
+
 @pytest.mark.parametrize("tier", [em.EXACT, em.F16, em.Q8])
 def test_batched_zipf_config3(dev, tier):
     """config 3: 64 tokens through the config-1 layer with a Zipf(1.1) router bias (skewed loads)"""
