@@ -17,7 +17,7 @@
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-#define G3_MF 5                // 32-row fragments a tile
+#define G3_MF 2                // 32-row fragments a tile
 #define GM_BM (32 * G3_MF)     // slots a tile (an expert's slots split into tiles of this many)
 #define G3_BM GM_BM
 
@@ -253,14 +253,14 @@ template <u32 F> struct BRow<F, true> {
   MDEV void f16(u32 jh, u32* o) const { p.f16(jh, o); }
 };
 
-// ---- the grouped GEMM, weights in registers. Block: 4 waves, a tile of up to G3_BM = 160 slots
-// (five 32-row fragments) x 256 weight rows (mode 0: 128 gate + 128 up features, mode 1: 256
+// ---- the grouped GEMM, weights in registers. Block: 4 waves, a tile of up to G3_BM = 64 slots
+// (two 32-row fragments) x 256 weight rows (mode 0: 128 gate + 128 up features, mode 1: 256
 // features); wave w owns 64 weight rows (mode 0: gate and up rows of features 32 w .. 32 w + 31, so
 // the SwiGLU epilogue pairs them in registers) for every slot of the tile. Each lane dequantizes its
 // own weight rows straight into the MFMA B operand: within a k-tile of 64 columns the K order is
 // permuted (MFMA k-slot 8 h + e of step s is column 32 h + 8 s + e, lane half h = lane / 32, for A
 // and B alike), so a lane's columns for the whole k-tile are one 32-column quant span, decoded once.
-// Only the activations go through LDS (two stages of 160 rows x 64 halves, padded to 72), read by
+// Only the activations go through LDS (two stages of 64 rows x 64 halves, padded to 72), read by
 // all four waves. The number of live fragments NL = ceil(rows / 32) is a compile-time variant, so
 // dead rows cost neither loads nor MFMAs. Three register slots rotate: at k-tile t a slot's weights
 // are decoded and multiplied, the next tile's activations are stored, and the slot is refilled with
@@ -393,16 +393,23 @@ DEV void gemm3_body(const GemmArgs& g, _Float16* lds, u32 e, u32 base, u32 m0, u
     }
 }
 
-// XCD-aware order: the hardware deals block b to XCD b % 8, so block b takes tile 8 ((b / 8) / NT) +
-// b % 8 and weight-row tile (b / 8) % NT: a tile's NT weight-row tiles all run on one XCD and read its
-// activation rows from that XCD's L2 (1-D grid, 8 NT ceil(tiles / 8) blocks)
+// XCD-aware order: the hardware deals block b to XCD b % 8. XCD x takes the contiguous chunk of the
+// tile list [x C, x C + C), C = ceil(tiles / 8), and walks it tile by tile, each tile's NT weight-row
+// tiles in a row (block b: tile x C + (b / 8) / NT, weight-row tile (b / 8) % NT). So a tile's blocks
+// share its activation rows in one L2, and an expert's consecutive slot tiles -- the same weights --
+// run on one XCD at about the same time and share its weight slices there (1-D grid,
+// 8 NT ceil(max tiles / 8) blocks). Blocks a CU: three on packed weights, two on GGUF rows (whose
+// wider per-lane loads need more registers) and for packed Q8_0 gate / up (which would spill at three).
+constexpr int g3_blocks(u32 F, u32 MODE, bool PKD) { return PKD && !(F == FM_Q8_0 && MODE == 0) ? 3 : 2; }
 template <u32 F, u32 MODE, bool PKD>
-__global__ void __launch_bounds__(256) k_moe_gemm3(GemmArgs g, u32 NT) {
+__global__ void __launch_bounds__(256, g3_blocks(F, MODE, PKD)) k_moe_gemm3(GemmArgs g, u32 NT) {
   extern __shared__ _Float16 lds[];
-  const u32 bi = blockIdx.x >> 3, tile = 8 * (bi / NT) + (blockIdx.x & 7), ntile = bi % NT;
+  const u32 q = blockIdx.x >> 3, ntile = q % NT;
+  const u32 ntl = g.tiles ? *g.ntiles : (g.M + G3_BM - 1) / G3_BM, C = (ntl + 7) / 8;
+  const u32 tile = (blockIdx.x & 7) * C + q / NT;
+  if (q / NT >= C || tile >= ntl) return;
   u32 e, m0, base, M;
   if (g.tiles) {
-    if (tile >= *g.ntiles) return;
     const u32 tv = g.tiles[tile];
     e = tv >> 16;
     m0 = (tv & 0xffffu) * G3_BM;
@@ -413,16 +420,10 @@ __global__ void __launch_bounds__(256) k_moe_gemm3(GemmArgs g, u32 NT) {
     m0 = tile * G3_BM;
     base = 0;
     M = g.M;
-    if (m0 >= M) return;
   }
-  const u32 rows = min(M - m0, (u32)G3_BM);
-  switch ((rows + 31) / 32) {  // block-uniform
-    case 1: gemm3_body<F, MODE, PKD, 1>(g, lds, e, base, m0, M, ntile); break;
-    case 2: gemm3_body<F, MODE, PKD, 2>(g, lds, e, base, m0, M, ntile); break;
-    case 3: gemm3_body<F, MODE, PKD, 3>(g, lds, e, base, m0, M, ntile); break;
-    case 4: gemm3_body<F, MODE, PKD, 4>(g, lds, e, base, m0, M, ntile); break;
-    default: gemm3_body<F, MODE, PKD, 5>(g, lds, e, base, m0, M, ntile); break;
-  }
+  static_assert(G3_MF == 2, "one or two live fragments");
+  if (M - m0 <= 32) gemm3_body<F, MODE, PKD, 1>(g, lds, e, base, m0, M, ntile);
+  else gemm3_body<F, MODE, PKD, 2>(g, lds, e, base, m0, M, ntile);
 }
 
 // y[t][r] = (sum_j, rank order, wt[t][j] out[inv[t nk + j]][r]) + sgo[t] shd[t][r] + x1[t][r]

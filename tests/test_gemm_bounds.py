@@ -10,7 +10,7 @@ A change to the kernel's addressing must be mirrored here.
 import numpy as np
 import pytest
 
-MF, BK, LD = 5, 64, 72
+MF, BK, LD = 2, 64, 72
 BM = 32 * MF
 STAGE = BM * LD  # halves
 
@@ -44,22 +44,23 @@ def check(ne, T, nk, K, N, mode, tiles=True, seed=0, skew=None):
     w, l = tid >> 6, tid & 63
     h, lr = l >> 5, l & 31
     bound = arows * K * 2
+    ntl = len(tl) if tiles else (T + BM - 1) // BM
+    C = (ntl + 7) // 8
+    seen = np.zeros((ntl, NT), np.int32)
     for b in range(nblk):
-        bi = b >> 3
-        tile = 8 * (bi // NT) + (b & 7)
-        ntile = bi % NT
+        q, ntile = b >> 3, (b >> 3) % NT
+        tile = (b & 7) * C + q // NT
+        if q // NT >= C or tile >= ntl:
+            continue
+        seen[tile, ntile] += 1
         if tiles:
-            if tile >= len(tl):
-                continue
             e, k = tl[tile]
             m0, base, M = k * BM, off[e], off[e + 1] - off[e]
         else:
             e, m0, base, M = 0, tile * BM, 0, T
-            if m0 >= M:
-                continue
         assert m0 < M and 0 <= e < ne
         rows = min(M - m0, BM)
-        NL = min((rows + 31) // 32, MF)
+        NL = 1 if M - m0 <= 32 else 2
         assert 1 <= NL <= MF and 32 * NL >= rows
         # A staging: chunk i = row 32 i + tid / 8, 16-byte chunk tid % 8
         for i in range(NL):
@@ -109,6 +110,7 @@ def check(ne, T, nk, K, N, mode, tiles=True, seed=0, skew=None):
                     for bb in range(2):
                         col = ntile * 256 + 64 * w + 32 * bb + lr
                         np.add.at(written, (s[ok], col[ok]), 1)
+    assert (seen == 1).all()  # every (tile, weight-row tile) exactly once
     # mode 0 writes N features of every slot; mode 1 all N rows
     assert (written == 1).all(), (written.min(), written.max())
     return nblk
