@@ -44,10 +44,10 @@ TRAFFIC_KERNELS = {
     "k_tree_rows<": ("c2_decode", "route"),
     "k_gu_topk<": ("c2_decode", "gate_up"),
     "k_dn_lane<": ("c2_decode", "down"),
-    "k_moe_gemm3<1u, 0u>": ("c1_prefill_2048", "gate_up"),
-    "k_moe_gemm3<1u, 1u>": ("c1_prefill_2048", "down"),
-    "k_moe_gemm3<3u, 0u>": ("c1k_prefill_2048", "gate_up"),
-    "k_moe_gemm3<4u, 1u>": ("c1k_prefill_2048", "down"),
+    "k_moe_gemm3<1u, 0u, true>": ("c1_prefill_2048", "gate_up"),
+    "k_moe_gemm3<1u, 1u, true>": ("c1_prefill_2048", "down"),
+    "k_moe_gemm3<3u, 0u, true>": ("c1k_prefill_2048", "gate_up"),
+    "k_moe_gemm3<4u, 1u, true>": ("c1k_prefill_2048", "down"),
 }
 
 

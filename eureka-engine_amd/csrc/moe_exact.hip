@@ -234,19 +234,33 @@ __global__ void __launch_bounds__(256) k_tree_rows_mt(TreeArgs a, u32 ntb) {
     }
     __syncthreads();
     if (j + 1 < ntb && t0 + TT < a.T) tree_mt_load_x<NSP, TT>(a, tid, t0 + TT, xl);  // next tile in flight
-    for (u32 tt = 0; tt < TT && t0 + tt < a.T; tt++) {
+    // every token of the tile (rows past T are zeros, their sums never stored): the in-lane levels
+    // first, then the six cross-lane levels of all 2 TT sums together -- independent chains, so the
+    // DPP and permlane latencies overlap -- and one store block
+    float v[TT][2];
+#pragma unroll
+    for (u32 tt = 0; tt < TT; tt++) {
       float4 xv[NQ];
 #pragma unroll
       for (u32 q = 0; q < NQ; q++) xv[q] = xsh4[tt * 64 * LS4 + L * LS4 + q];
 #pragma unroll
       for (u32 k = 0; k < 2; k++) {
-        if (!has[k]) continue;
         float n[NQ];
 #pragma unroll
         for (u32 q = 0; q < NQ; q++) n[q] = leaf4(wr[k] + 4 * q, xv[q]);
-        const float v = tree64_asc(live ? tree_in_lane<NQ>(n) : 0.0f);  // a dead lane's leaves are +0 pads
-        if (L == 0) op[k][(u64)(t0 + tt) * ost[k]] = hb[k] ? v + bia[k] : v;
+        v[tt][k] = live ? tree_in_lane<NQ>(n) : 0.0f;  // a dead lane's leaves are +0 pads
       }
+    }
+#pragma unroll
+    for (u32 tt = 0; tt < TT; tt++)
+#pragma unroll
+      for (u32 k = 0; k < 2; k++) v[tt][k] = tree64_asc(v[tt][k]);
+    if (L == 0) {
+#pragma unroll
+      for (u32 tt = 0; tt < TT; tt++)
+#pragma unroll
+        for (u32 k = 0; k < 2; k++)
+          if (has[k] && t0 + tt < a.T) op[k][(u64)(t0 + tt) * ost[k]] = hb[k] ? v[tt][k] + bia[k] : v[tt][k];
     }
   }
 }
@@ -997,6 +1011,19 @@ __global__ void __launch_bounds__(256) k_dequant(const u8* __restrict__ W, u64 r
 
 #define FM_CASES(X) X(FM_Q8_0) X(FM_Q4_K) X(FM_Q6_K) X(FM_Q5_K)
 
+// compute units of the current device (queried once)
+static u32 cu_count() {
+  static u32 n = 0;
+  if (!n) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      n = (u32)v;
+    else
+      n = 256;
+  }
+  return n;
+}
+
 int launch_tree_rows(const TreeArgs& a, u32 nsp, hipStream_t st) {
   u32 rows = 0;
   for (u32 i = 0; i < a.nseg; i++) rows += a.seg[i].rows;
@@ -1004,10 +1031,16 @@ int launch_tree_rows(const TreeArgs& a, u32 nsp, hipStream_t st) {
   if (a.T >= 16 && nsp <= 2) {  // token tiles: weights read once a tile
     const u32 tt = nsp == 1 ? 8u : 4u;
     const size_t sm = (size_t)tt * 64 * (32 * nsp + 4) * 4;
-    // tiles a block: about two blocks a CU over the whole grid, at least one tile each
-    const u32 rb = (rows + 7) / 8, nt = (a.T + tt - 1) / tt;
-    u32 ntb = rb * nt / 512;
-    ntb = ntb < 1 ? 1 : ntb > nt ? nt : ntb;
+    // tiles a block: the count that minimises (rounds of resident blocks) x (tiles a block + 2, a
+    // block's own cost of loading its rows and filling its pipeline), two blocks resident a CU -- a
+    // grid just past one round of blocks would otherwise take two
+    const u32 rb = (rows + 7) / 8, nt = (a.T + tt - 1) / tt, slots = 2 * cu_count();
+    u32 ntb = 1;
+    u64 best = ~0ull;
+    for (u32 n = 1; n <= nt; n++) {
+      const u64 blocks = (u64)rb * ((nt + n - 1) / n), cost = (blocks + slots - 1) / slots * (n + 2);
+      if (cost < best) { best = cost; ntb = n; }
+    }
     const dim3 grid(rb, (nt + ntb - 1) / ntb);
     static bool set1 = false, set2 = false;
     if (nsp == 1) {

@@ -10,13 +10,22 @@ import numpy as np
 import pytest
 
 
-def launch(nsp, T, rows):
+def launch(nsp, T, rows, cus=256):
     """launch_tree_rows' choice for T >= 16, nsp <= 2: TT, dynamic LDS bytes, ntb, grid"""
     tt = 8 if nsp == 1 else 4
     sm = tt * 64 * (32 * nsp + 4) * 4
-    rb, nt = (rows + 7) // 8, (T + tt - 1) // tt
-    ntb = min(max(rb * nt // 512, 1), nt)
+    rb, nt, slots = (rows + 7) // 8, (T + tt - 1) // tt, 2 * cus
+    ntb, best = 1, None
+    for n in range(1, nt + 1):
+        cost = (rb * ((nt + n - 1) // n) + slots - 1) // slots * (n + 2)
+        if best is None or cost < best:
+            ntb, best = n, cost
     return tt, sm, ntb, (rb, (nt + ntb - 1) // ntb)
+
+
+def test_tree_mt_tiles_a_block():
+    assert launch(1, 513, 513)[2] == 10   # config 5: 65 x 7 blocks in one round, not 65 x 9 in two
+    assert launch(1, 2048, 128)[2] == 8   # the 2048-token prefill: 16 x 32 blocks, one round
 
 
 def check(nsp, cols, T, segrows, wfmt_bytes=4):
@@ -91,5 +100,5 @@ def test_tree_mt_grid_covers_tokens():
     for T in (16, 17, 63, 64, 513, 2047, 2048, 4096):
         for rows in (1, 8, 129, 513, 1024):
             for nsp in (1, 2):
-                TT, _, ntb, (gx, gy) = launch(nsp, T, rows)
+                TT, _, ntb, (gx, gy) = launch(nsp, T, rows, cus=(256, 80, 304)[(T + rows) % 3])
                 assert gy * ntb * TT >= T and (gy - 1) * ntb * TT < T
