@@ -7,7 +7,7 @@ top-8, expert ff 512, shared expert 512, gate/up Q4_K, down Q6_K -- decoding one
 A step = one token through the 40 layers; value = microseconds per token-layer.
 
   python bench.py [--steps K] [--warmup W] [--layers L] [--config c2] [--tier exact|q8] [--no-cpu]
-                  [--legs batched,prefill,prefill_k,c5]
+                  [--legs batched,prefill,prefill_k,c5,rmsnorm]
   python bench.py --copy-calib          (the PMC byte-counter calibration copies only)
   python bench.py --traffic-from DIR    (profiles/traffic.json from rocprofv3 FETCH_SIZE / WRITE_SIZE passes)
 """
@@ -184,6 +184,35 @@ def batched(dev, shape, T, layers, steps, warmup, tier):
             "hbm_frac_last_layer": round(byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def rmsnorm_leg(dev, n, steps=50):
+    """llb_moe_hip_rmsnorm_add (the router's input step): microseconds a call for one decode row, and
+    HBM bytes / time for a 2048-row chunk (x, z read, x1, h2 written: 16 bytes a column a row)"""
+    out = {}
+    for T in (1, 2048):
+        bufs = [dev.alloc(T * n * 4) for _ in range(4)]
+        w = dev.alloc(n * 4)
+        dev.check(dev.lib.llb_moe_hip_gen_gauss(0, 900, 0, T * n, 1.0, bufs[0]))
+        dev.check(dev.lib.llb_moe_hip_gen_gauss(0, 901, 0, T * n, 1.0, bufs[1]))
+        dev.check(dev.lib.llb_moe_hip_gen_gauss(0, 902, 0, n, 1.0, w))
+        call = lambda: dev.check(dev.lib.llb_moe_hip_rmsnorm_add(bufs[0], bufs[1], w, 1e-6, T, n, bufs[2], bufs[3]))  # noqa: E731
+        call()
+        dev.sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            call()
+        dev.sync()
+        us = (time.perf_counter() - t0) / steps * 1e6
+        for b in bufs + [w]:
+            dev.free(b)
+        if T == 1:
+            out["us_per_call_T1"] = round(us, 2)
+        else:
+            gbs = 16.0 * T * n / (us * 1e-6) / 1e9
+            out["T2048"] = {"us": round(us, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    out["config"] = f"n = {n}, eps 1e-6, back-to-back eager calls (the T = 1 figure includes launch)"
+    return out
+
+
 def cpu_baseline(shape, seconds=12.0):
     """the CPU oracle's exact layer, single thread, on tokens of layer 0 (experts generated first)."""
     import oracle_lib as ol
@@ -222,8 +251,8 @@ def main():
     ap.add_argument("--prefill-T", type=int, default=2048)
     ap.add_argument("--no-c5", dest="c5", action="store_false",
                     help="skip the config-5 leg (48 resident 512-expert layers, 1 + 512 tokens a launch)")
-    ap.add_argument("--legs", default="batched,prefill,prefill_k,c5",
-                    help="legs after the decode line: batched (config 3), prefill (c1), prefill_k (c1k), c5")
+    ap.add_argument("--legs", default="batched,prefill,prefill_k,c5,rmsnorm",
+                    help="legs after the decode line: batched (config 3), prefill (c1), prefill_k (c1k), c5, rmsnorm")
     ap.add_argument("--traffic-from", metavar="DIR",
                     help="only write profiles/traffic.json from the PMC csv directories under DIR and exit")
     ap.add_argument("--copy-calib", action="store_true",
@@ -349,6 +378,8 @@ def main():
         c5["tokens_per_s"] = round(513 / (c5["us_per_layer"] * 1e-6), 1)
         c5["config"] = "c5: 48 layers x 512 experts top-10 (Q4_K gate/up, Q6_K down, shared expert), 1 + 512 tokens a launch, f16 tier, packed stacks"
         out["c5_mixed"] = c5
+    if "rmsnorm" in legs:
+        out["rmsnorm_add"] = rmsnorm_leg(dev, shape.dm)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(shape)
     print(json.dumps(out), flush=True)

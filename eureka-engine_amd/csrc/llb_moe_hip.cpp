@@ -701,6 +701,16 @@ int llb_moe_hip_group(llb_dptr ids, uint32_t n, uint32_t nk, uint32_t ne, llb_dp
                   "group");
 }
 
+int llb_moe_hip_rmsnorm_add(llb_dptr x, llb_dptr z, llb_dptr w, float eps, uint32_t T, uint32_t n, llb_dptr x1,
+                            llb_dptr h2) {
+  if (!x || !z || !w || !h2) return fail(LLB_HIP_EINVAL, "rmsnorm_add: null operand");
+  if (n == 0 || n > 16384 || T == 0 || (n > 512 && n % 4))
+    return fail(LLB_HIP_EINVAL, "rmsnorm_add: 1 <= n <= 16384, n % 4 == 0 past 512, T >= 1");
+  return launched(launch_rmsnorm_add(dp<float>(x), dp<float>(z), dp<float>(w), eps, T, n, dp<float>(x1), dp<float>(h2),
+                                     g_stream),
+                  "rmsnorm_add");
+}
+
 int llb_moe_hip_q8_1(llb_dptr x, uint32_t n, llb_dptr q, llb_dptr ds) {
   if (n % 32) return fail(LLB_HIP_EINVAL, "q8_1: n % 32 != 0");
   return launched(launch_q8_1(dp<float>(x), n, dp<int8_t>(q), dp<float2>(ds), g_stream), "q8_1");

@@ -1007,6 +1007,93 @@ __global__ void __launch_bounds__(256) k_dequant(const u8* __restrict__ W, u64 r
   for (u32 k = 0; k < 32; k++) o[k] = w[k];
 }
 
+// ---------------------------------------------------------------- llb_rmsnorm_add (the step before the router)
+
+// tools/payload-fuse.patch:106-127 and its other widths (tools/payload-w1024.patch:130-150,
+// tools/payload-anyshape.patch:300-340): x1 = x + z; the squares of x1 summed by one balanced pairwise
+// tree in column order over a power of two >= n (the reference's 1024 threads x 4, 8 or L leaves with
+// +0 past n, then rms_tree's lane pairs t, t + 1, then t, t + 2 ...); s = 1 / sqrt(sum / n + eps), each op
+// rounded once; h2 = (x1 s) w. One block of 256 a row: thread t holds leaves Q t .. Q t + Q - 1 of the
+// tree over 256 Q >= n (the same sums: the extra leaves are +0), the in-lane levels, then tree64_asc
+// across the wave (exact on lane 0), then the four waves as (w0 + w1) + (w2 + w3).
+template <u32 Q>
+__global__ void __launch_bounds__(256) k_rmsnorm_add(const float* __restrict__ x, const float* __restrict__ z,
+                                                     const float* __restrict__ w, float eps, u32 n,
+                                                     float* __restrict__ x1, float* __restrict__ h2) {
+  __shared__ float ws[4];
+  const u32 t = threadIdx.x, r = blockIdx.x;
+  const float* xr = x + (u64)r * n;
+  const float* zr = z + (u64)r * n;
+  // the thread's leaves stay in registers for the output pass: one read of x and z
+  float v[Q], b[Q];
+  if constexpr (Q % 4 == 0) {  // n % 4 == 0 here (launcher): whole float4s, all in or all out
+#pragma unroll
+    for (u32 k = 0; k < Q; k += 4) {
+      const u32 i = t * Q + k;
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f), c = a;
+      if (i < n) {
+        a = *(const float4*)(xr + i);
+        c = *(const float4*)(zr + i);
+      }
+      v[k] = a.x + c.x; v[k + 1] = a.y + c.y; v[k + 2] = a.z + c.z; v[k + 3] = a.w + c.w;
+    }
+  } else {
+#pragma unroll
+    for (u32 k = 0; k < Q; k++) {
+      const u32 i = t * Q + k;
+      v[k] = i < n ? xr[i] + zr[i] : 0.0f;
+    }
+  }
+#pragma unroll
+  for (u32 k = 0; k < Q; k++) b[k] = t * Q + k < n ? v[k] * v[k] : 0.0f;
+#pragma unroll
+  for (u32 st = 1; st < Q; st <<= 1)
+#pragma unroll
+    for (u32 k = 0; k < Q; k += 2 * st) b[k] = b[k] + b[k + st];
+  const float sw = tree64_asc(b[0]);
+  if ((t & 63) == 0) ws[t >> 6] = sw;
+  __syncthreads();
+  const float sum = (ws[0] + ws[1]) + (ws[2] + ws[3]);
+  // correctly rounded division and square root (HIP's / and __builtin_sqrtf; its __fsqrt_rn is the
+  // native approximation unless OCML_BASIC_ROUNDED_OPERATIONS is set)
+  const float s = 1.0f / __builtin_sqrtf(sum / (float)n + eps);
+  if constexpr (Q % 4 == 0) {
+#pragma unroll
+    for (u32 k = 0; k < Q; k += 4) {
+      const u32 i = t * Q + k;
+      if (i < n) {
+        const float4 wv = *(const float4*)(w + i);
+        if (x1) *(float4*)(x1 + (u64)r * n + i) = make_float4(v[k], v[k + 1], v[k + 2], v[k + 3]);
+        *(float4*)(h2 + (u64)r * n + i) = make_float4((v[k] * s) * wv.x, (v[k + 1] * s) * wv.y, (v[k + 2] * s) * wv.z,
+                                                      (v[k + 3] * s) * wv.w);
+      }
+    }
+  } else {
+#pragma unroll
+    for (u32 k = 0; k < Q; k++) {
+      const u32 i = t * Q + k;
+      if (i < n) {
+        if (x1) x1[(u64)r * n + i] = v[k];
+        h2[(u64)r * n + i] = (v[k] * s) * w[i];
+      }
+    }
+  }
+}
+
+int launch_rmsnorm_add(const float* x, const float* z, const float* w, float eps, u32 T, u32 n, float* x1, float* h2,
+                       hipStream_t st) {
+  if (n == 0 || n > 16384 || T == 0) return -1;
+  u32 P = 256;
+  while (P < n) P <<= 1;
+  if (P >= 1024 && n % 4) return -1;  // the float4 path takes whole quads
+  const dim3 grid(T);
+#define RN_L(Qv) \
+  if (P == 256 * Qv) { LAUNCH_K((k_rmsnorm_add<Qv>), grid, dim3(256), 0, st, x, z, w, eps, n, x1, h2); return 0; }
+  RN_L(1) RN_L(2) RN_L(4) RN_L(8) RN_L(16) RN_L(32) RN_L(64)
+#undef RN_L
+  return -1;
+}
+
 // ---------------------------------------------------------------- launchers
 
 #define FM_CASES(X) X(FM_Q8_0) X(FM_Q4_K) X(FM_Q6_K) X(FM_Q5_K)

@@ -124,6 +124,8 @@ struct GemmArgs {
 };
 int launch_moe_gemm(const GemmArgs& g, uint32_t fm, uint32_t mode, uint32_t grid_y, hipStream_t st);
 uint32_t gemm_bm();
+int launch_rmsnorm_add(const float* x, const float* z, const float* w, float eps, uint32_t T, uint32_t n, float* x1,
+                       float* h2, hipStream_t st);
 uint64_t pack_bytes(uint32_t fm, uint32_t R, uint32_t K);
 int launch_pack(uint32_t fm, const uint8_t* W, uint64_t es, uint64_t rb, uint32_t R, uint32_t K, uint32_t ne,
                 uint8_t* P, hipStream_t st);

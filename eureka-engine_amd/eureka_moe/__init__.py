@@ -77,6 +77,8 @@ _SIGS = {
     "llb_moe_hip_group": (C.c_int, [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64,
                                     C.c_uint64, C.c_size_t]),
     "llb_moe_hip_q8_1": (C.c_int, [C.c_uint64, C.c_uint32, C.c_uint64, C.c_uint64]),
+    "llb_moe_hip_rmsnorm_add": (C.c_int, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_float, C.c_uint32, C.c_uint32,
+                                          C.c_uint64, C.c_uint64]),
     "llb_moe_hip_dequant": (C.c_int, [C.c_uint32, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint64]),
     "llb_moe_hip_timing": (C.c_int, [C.c_int]),
     "llb_hip_spin": (C.c_int, [C.c_uint32]),

@@ -128,6 +128,11 @@ size_t llb_moe_hip_pack_bytes(const llb_moe_layer* L);
 int llb_moe_hip_pack(llb_moe_layer* L, llb_dptr buf, size_t bytes);
 
 /* ---- kernel-level entry points ---- */
+/* llb_rmsnorm_add (tools/payload-fuse.patch:106-127; host/llb_host.c's gpu_rnadd), the step that makes
+ * the router's input, for T rows of n <= 16384 (a multiple of 4 past 512): x1 = x + z, h2 = (x1 s) w, s = 1 / sqrt(sum x1^2 / n +
+ * eps), the sum in the reference kernels' tree order. x, z, x1, h2: [T][n] f32 (x1 may be 0); w: [n]. */
+int llb_moe_hip_rmsnorm_add(llb_dptr x, llb_dptr z, llb_dptr w, float eps, uint32_t T, uint32_t n, llb_dptr x1,
+                            llb_dptr h2);
 /* llb_moe_topk block 0 (tools/payload-moeany.patch:311-470) for T tokens: lg [T][lstride] (ne logits,
  * then the shared gate's at index ne when has_sg) -> ids, wt [T][nk], sgo [T] */
 int llb_moe_hip_topk(llb_dptr lg, uint32_t lstride, uint32_t T, uint32_t ne, uint32_t nk, uint32_t has_sg,

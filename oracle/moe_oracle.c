@@ -711,3 +711,34 @@ int mo_moe_f64(const mo_layer* L, u32 T, const float* h2, const u32* ids, double
   free(w); free(lg); free(act);
   return 0;
 }
+
+/* ---- llb_rmsnorm_add, the step before the router (tools/payload-fuse.patch:106-127, which takes
+ * n = 4096 as 1024 threads x 4 leaves; tools/payload-w1024.patch:130-150 and
+ * tools/payload-anyshape.patch:300-340 give the other widths 8 leaves a thread, or rms_wide's L, over a
+ * tree of 1024 x that many leaves with +0 past n; rms_tree, tools/payload-fuse.patch:76-103, pairs
+ * lanes t, t + 1, then t, t + 2, ..., then the warp sums the same way). Every branch is one balanced
+ * pairwise tree in column order over a power of two >= n, whose +0 leaves leave the sums of squares
+ * unchanged -- so: the tree over the next power of two >= n. Then s = 1 / sqrt(sum / n + eps) (each op
+ * rounded once), x1 = x + z, h2 = (x1 s) w. */
+static float rn_tree(const float* x, const float* z, u32 lo, u32 len, u32 n) {
+  if (len == 1) {
+    if (lo >= n) return 0.0f;
+    const float v = x[lo] + z[lo];
+    return v * v;
+  }
+  const float a = rn_tree(x, z, lo, len / 2, n);
+  const float b = rn_tree(x, z, lo + len / 2, len / 2, n);
+  return a + b;
+}
+float mo_rmsnorm_add(const float* x, const float* z, const float* w, float eps, u32 n, float* x1, float* h2) {
+  u32 P = 1;
+  while (P < n) P <<= 1;
+  const float sum = rn_tree(x, z, 0, P, n);
+  const float s = 1.0f / sqrtf(sum / (float)n + eps);
+  for (u32 i = 0; i < n; i++) {
+    const float v = x[i] + z[i];
+    if (x1) x1[i] = v;
+    h2[i] = (v * s) * w[i];
+  }
+  return s;
+}

@@ -93,6 +93,9 @@ int mo_moe_f64(const mo_layer* L, uint32_t T, const float* h2, const uint32_t* i
 
 /* q8_1 activations, pf_q8x / ref_q8x: per 32 values d = amax / 127, q = round(x / d), s = sum x */
 void mo_q8_1(const float* x, uint32_t n, int8_t* q, float* d, float* s);
+/* llb_rmsnorm_add (tools/payload-fuse.patch:106-127): x1 = x + z (x1 may be NULL), h2 = (x1 s) w,
+ * s = 1 / sqrt(tree sum of x1^2 / n + eps), returned */
+float mo_rmsnorm_add(const float* x, const float* z, const float* w, float eps, uint32_t n, float* x1, float* h2);
 float mo_dot_q8(uint32_t fm, const uint8_t* row, uint32_t cols, const int8_t* q, const float* d,
                 const float* s);
 

@@ -13,3 +13,8 @@ void ref_deq_row(int fmt, const uint8_t* row, int cols, float* out) { deq_row(fm
 float ref_hf_exp(float x) { return hf_exp(x); }
 float ref_hf_silu(float x) { return hf_silu(x); }
 float ref_hf_sigmoid(float x) { return hf_sigmoid(x); }
+/* rms_norm (tools/qwen35_engine.c:510-515) with its EPS set for the call */
+void ref_rms_norm(float* h, const float* x, const float* w, int n, float eps) {
+  EPS = eps;
+  rms_norm(h, x, w, n);
+}

@@ -58,6 +58,7 @@ _SIGS = {
     "mo_moe_f64": (C.c_int, [C.POINTER(MoLayer), C.c_uint32, P, P, P]),
     "mo_q8_1": (None, [P, C.c_uint32, P, P, P]),
     "mo_dot_q8": (C.c_float, [C.c_uint32, P, C.c_uint32, P, P, P]),
+    "mo_rmsnorm_add": (C.c_float, [P, P, P, C.c_float, C.c_uint32, P, P]),
 }
 
 _lib = None
@@ -85,7 +86,20 @@ def ref_lib():
     r.ref_deq_row.restype, r.ref_deq_row.argtypes = None, [C.c_int, P, C.c_int, P]
     for n in ("ref_hf_exp", "ref_hf_silu", "ref_hf_sigmoid"):
         getattr(r, n).restype, getattr(r, n).argtypes = C.c_float, [C.c_float]
+    r.ref_rms_norm.restype, r.ref_rms_norm.argtypes = None, [P, P, P, C.c_int, C.c_float]
     return r
+
+
+def rmsnorm_add(x, z, w, eps):
+    """mo_rmsnorm_add over the rows of x, z ([T][n] f32): (x1, h2, s per row)"""
+    x, z, w = (np.ascontiguousarray(a, np.float32) for a in (x, z, w))
+    T, n = x.shape
+    x1, h2, s = np.zeros_like(x), np.zeros_like(x), np.zeros(T, np.float32)
+    for t in range(T):
+        xt, zt, x1t, h2t = x[t].copy(), z[t].copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+        s[t] = lib().mo_rmsnorm_add(ptr(xt), ptr(zt), ptr(w), eps, n, ptr(x1t), ptr(h2t))
+        x1[t], h2[t] = x1t, h2t
+    return x1, h2, s
 
 
 def ptr(a):

@@ -392,3 +392,28 @@ def test_batched_zipf_config3(dev, tier):
         m = ol.err_metrics(y - x1, yr - x1)
         _say("vs oracle", m)
         assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999
+
+
+@pytest.mark.parametrize("n", [100, 257, 1000, 1024, 1536, 2048, 4096, 5120, 16384])
+def test_rmsnorm_add_bit_exact(dev, n):
+    """llb_moe_hip_rmsnorm_add (tools/payload-fuse.patch:106-127) against the oracle, bit for bit: x1, h2;
+    three rows, the last one zero (s = 1 / sqrt(eps))"""
+    _say("rmsnorm_add", n)
+    rng = np.random.default_rng(n)
+    T = 3
+    x = (rng.standard_normal((T, n)) * 4).astype(np.float32)
+    z = rng.standard_normal((T, n)).astype(np.float32)
+    x[2] = 0.0
+    z[2] = 0.0
+    w = (1 + 0.2 * rng.standard_normal(n)).astype(np.float32)
+    eps = np.float32(1e-6)
+    px, pz, pw = dev.upload(x), dev.upload(z), dev.upload(w)
+    px1, ph2 = dev.alloc(T * n * 4), dev.alloc(T * n * 4)
+    dev.check(dev.lib.llb_moe_hip_rmsnorm_add(px, pz, pw, eps, T, n, px1, ph2))
+    x1 = dev.read(px1, (T, n), np.float32)
+    h2 = dev.read(ph2, (T, n), np.float32)
+    for p in (px, pz, pw, px1, ph2):
+        dev.free(p)
+    rx1, rh2, _ = ol.rmsnorm_add(x, z, w, eps)
+    assert np.array_equal(x1.view(np.uint32), rx1.view(np.uint32))
+    assert np.array_equal(h2.view(np.uint32), rh2.view(np.uint32)), np.abs(h2 - rh2).max()
