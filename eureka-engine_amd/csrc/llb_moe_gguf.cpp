@@ -1,0 +1,497 @@
+// llb_moe_gguf.cpp -- GGUF expert stacks into the layer (llb_moe_load / moe_fill,
+// host/llb_host.c:446-586; llb_gg_tensor, host/llb_gguf.c:854-865). Host code.
+//
+// The file is read with pread: the header (metadata and tensor table) is parsed with every length and
+// count checked against the file size, then tensors are found by name. A layer's stacks are
+// blk.N.ffn_gate_exps / ffn_up_exps / ffn_down_exps (or ffn_gate_up_exps for the fused stack), checked
+// against the layer's declared formats and byte counts as the reference does, and placed:
+//   device  hipMalloc + pread in 64 MiB pieces + upload (the reference's mode 0);
+//   host    pinned, device-mapped host memory (hipHostMalloc mapped | portable), pread in place (mode 1);
+//   stream  the file mapped read-only; per decoded token the k chosen experts are copied into device
+//           staging slots and the experts run on slot ids 0..k-1 (mode 2; llb_moe_hip_forward does it).
+// The router (ffn_gate_inp), the shared gate row (ffn_gate_inp_shexp) and the shared expert
+// (ffn_{gate,up,down}_shexp) are loaded the same way when the file holds them and the layer does not
+// already point at them (the reference takes those from its pack; a GGUF-only caller takes them here).
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/llb_moe_hip.h"
+#include "moe_kernels.h"
+
+uint64_t llb_row_bytes(uint32_t fm, uint32_t cols);
+#define row_bytes llb_row_bytes
+
+struct GgTensor {
+  std::string name;
+  uint32_t type, nd;
+  uint64_t dims[4];
+  uint64_t off;    // from the file start
+  uint64_t bytes;
+};
+struct llb_gguf {
+  int fd;
+  uint64_t size;
+  uint32_t version, alignment;
+  std::vector<GgTensor> t;
+};
+
+// ggml type -> (block bytes, block elements); 0 for types this path does not read
+static bool gg_block(uint32_t ty, uint64_t& bb, uint64_t& be) {
+  switch (ty) {
+    case 0: bb = 4; be = 1; return true;      // F32
+    case 1: bb = 2; be = 1; return true;      // F16
+    case 8: bb = 34; be = 32; return true;    // Q8_0
+    case 12: bb = 144; be = 256; return true; // Q4_K
+    case 13: bb = 176; be = 256; return true; // Q5_K
+    case 14: bb = 210; be = 256; return true; // Q6_K
+    case 30: bb = 2; be = 1; return true;     // BF16
+    default: return false;
+  }
+}
+// ggml type -> LLB_FM_* (host/llb_formats.h:5-14); -1 when the path has no decoder for it
+static int gg_fm(uint32_t ty) {
+  switch (ty) {
+    case 0: return LLB_FM_F32;
+    case 8: return LLB_FM_Q8_0;
+    case 12: return LLB_FM_Q4_K;
+    case 13: return LLB_FM_Q5_K;
+    case 14: return LLB_FM_Q6_K;
+    default: return -1;
+  }
+}
+
+struct Rd {
+  int fd;
+  uint64_t size, pos;
+  bool bad;
+  bool get(void* p, uint64_t n) {
+    if (bad || n > size || pos > size - n) return (bad = true, false);
+    uint8_t* q = (uint8_t*)p;
+    for (uint64_t k = 0; k < n;) {
+      const ssize_t r = pread(fd, q + k, (size_t)(n - k), (off_t)(pos + k));
+      if (r <= 0) return (bad = true, false);
+      k += (uint64_t)r;
+    }
+    pos += n;
+    return true;
+  }
+  template <class T> T v() {
+    T x{};
+    get(&x, sizeof x);
+    return x;
+  }
+  bool str(std::string* s) {
+    const uint64_t n = v<uint64_t>();
+    if (bad || n > (1u << 20) || n > size - pos) return (bad = true, false);
+    if (!s) return (pos += n, true);
+    s->resize((size_t)n);
+    return get(&(*s)[0], n);
+  }
+  // skips a metadata value of type ty (arrays nest at most 4 deep)
+  bool skip(uint32_t ty, int depth = 0) {
+    static const uint8_t sz[13] = {1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8};
+    if (ty == 8) return str(nullptr);
+    if (ty == 9) {
+      const uint32_t et = v<uint32_t>();
+      const uint64_t n = v<uint64_t>();
+      if (bad || depth >= 4 || et > 12) return (bad = true, false);
+      if (et != 8 && et != 9) {
+        if (n > (size - pos) / sz[et]) return (bad = true, false);
+        pos += n * sz[et];
+        return true;
+      }
+      for (uint64_t i = 0; i < n && !bad; i++) skip(et, depth + 1);
+      return !bad;
+    }
+    if (ty > 12) return (bad = true, false);
+    if (sz[ty] > size - pos) return (bad = true, false);
+    pos += sz[ty];
+    return true;
+  }
+};
+
+extern "C" {
+
+llb_gguf* llb_gguf_open(const char* path) {
+  if (!path) return (llb_fail_msg(LLB_HIP_EINVAL, "gguf: null path"), nullptr);
+  const int fd = open(path, O_RDONLY);
+  if (fd < 0) return (llb_fail_msg(LLB_HIP_EINVAL, "gguf: cannot open the file"), nullptr);
+  struct stat st;
+  if (fstat(fd, &st) != 0) {
+    close(fd);
+    return (llb_fail_msg(LLB_HIP_EINVAL, "gguf: cannot stat the file"), nullptr);
+  }
+  Rd r{fd, (uint64_t)st.st_size, 0, false};
+  const uint32_t magic = r.v<uint32_t>(), version = r.v<uint32_t>();
+  const uint64_t nt = r.v<uint64_t>(), nkv = r.v<uint64_t>();
+  const char* why = nullptr;
+  if (r.bad || magic != 0x46554747u) why = "gguf: not a GGUF file";
+  else if (version < 2 || version > 3) why = "gguf: only versions 2 and 3";
+  else if (nt > (1u << 24) || nkv > (1u << 24)) why = "gguf: implausible tensor or key count";
+  uint32_t alignment = 32;
+  for (uint64_t i = 0; !why && i < nkv; i++) {
+    std::string key;
+    r.str(&key);
+    const uint32_t ty = r.v<uint32_t>();
+    if (key == "general.alignment" && ty == 4) {
+      alignment = r.v<uint32_t>();
+      if (alignment == 0 || (alignment & (alignment - 1))) why = "gguf: general.alignment not a power of two";
+    } else {
+      r.skip(ty);
+    }
+    if (r.bad) why = "gguf: truncated or malformed metadata";
+  }
+  auto* g = new llb_gguf{fd, (uint64_t)st.st_size, version, alignment, {}};
+  if (!why) g->t.reserve((size_t)nt);
+  for (uint64_t i = 0; !why && i < nt; i++) {
+    GgTensor t{};
+    r.str(&t.name);
+    t.nd = r.v<uint32_t>();
+    if (r.bad || t.nd == 0 || t.nd > 4) {
+      why = "gguf: malformed tensor table";
+      break;
+    }
+    uint64_t ne = 1;
+    for (uint32_t d = 0; d < t.nd; d++) {
+      t.dims[d] = r.v<uint64_t>();
+      if (t.dims[d] == 0 || t.dims[d] > (1ull << 40) || ne > (1ull << 48) / t.dims[d]) why = "gguf: implausible tensor shape";
+      else ne *= t.dims[d];
+    }
+    t.type = r.v<uint32_t>();
+    t.off = r.v<uint64_t>();
+    if (r.bad) why = "gguf: truncated tensor table";
+    uint64_t bb = 0, be = 1;
+    if (!why && gg_block(t.type, bb, be)) {
+      if (t.dims[0] % be) why = "gguf: a row is not whole blocks";
+      else t.bytes = ne / be * bb;
+    }
+    g->t.push_back(t);
+  }
+  if (!why) {
+    const uint64_t data = (r.pos + alignment - 1) / alignment * alignment;
+    for (auto& t : g->t) {
+      if (t.off % alignment || t.off > g->size || data > g->size - t.off) {
+        why = "gguf: a tensor offset outside the file";
+        break;
+      }
+      t.off += data;
+      if (t.bytes > g->size - t.off) {
+        why = "gguf: a tensor runs past the end of the file";
+        break;
+      }
+    }
+  }
+  if (why) {
+    close(fd);
+    delete g;
+    return (llb_fail_msg(LLB_HIP_EINVAL, why), nullptr);
+  }
+  return g;
+}
+
+void llb_gguf_close(llb_gguf* g) {
+  if (!g) return;
+  close(g->fd);
+  delete g;
+}
+
+uint64_t llb_gguf_count(const llb_gguf* g) { return g ? g->t.size() : 0; }
+
+int llb_gguf_tensor_at(const llb_gguf* g, uint64_t i, char* name, size_t cap, uint64_t* offset, uint64_t* bytes,
+                       uint32_t* type, uint32_t* nd, uint64_t* dims) {
+  if (!g || i >= g->t.size()) return llb_fail_msg(LLB_HIP_EINVAL, "gguf: no such tensor index");
+  const GgTensor& t = g->t[i];
+  if (name && cap) snprintf(name, cap, "%s", t.name.c_str());
+  if (offset) *offset = t.off;
+  if (bytes) *bytes = t.bytes;
+  if (type) *type = t.type;
+  if (nd) *nd = t.nd;
+  if (dims)
+    for (uint32_t d = 0; d < 4; d++) dims[d] = d < t.nd ? t.dims[d] : 1;
+  return 0;
+}
+
+int llb_gguf_find(const llb_gguf* g, const char* name) {
+  if (!g || !name) return -1;
+  for (size_t i = 0; i < g->t.size(); i++)
+    if (g->t[i].name == name) return (int)i;
+  return -1;
+}
+
+}  // extern "C"
+
+// one stack's bytes into its residency (moe_fill, host/llb_host.c:445-487)
+static int fill(const llb_gguf* g, const GgTensor& t, int mode, llb_dptr* out, const char* what) {
+  char msg[256];
+  if (mode == LLB_MOE_RES_HOST) {
+    void* h = nullptr;
+    if (hipHostMalloc(&h, t.bytes, hipHostMallocMapped | hipHostMallocPortable) != hipSuccess) {
+      snprintf(msg, sizeof msg, "gguf: cannot pin %llu bytes of host memory for %s", (unsigned long long)t.bytes, what);
+      return llb_fail_msg(LLB_HIP_EDEVICE, msg);
+    }
+    for (uint64_t k = 0; k < t.bytes;) {
+      const uint64_t c = t.bytes - k > (1ull << 30) ? (1ull << 30) : t.bytes - k;
+      const ssize_t r = pread(g->fd, (uint8_t*)h + k, (size_t)c, (off_t)(t.off + k));
+      if (r <= 0) {
+        (void)hipHostFree(h);
+        return llb_fail_msg(LLB_HIP_EINVAL, "gguf: read failed");
+      }
+      k += (uint64_t)r;
+    }
+    void* dp = nullptr;
+    if (hipHostGetDevicePointer(&dp, h, 0) != hipSuccess) {
+      (void)hipHostFree(h);
+      return llb_fail_msg(LLB_HIP_EDEVICE, "gguf: no device address for the pinned stack");
+    }
+    *out = (llb_dptr)(uintptr_t)dp;
+    return 0;
+  }
+  void* d = nullptr;
+  if (hipMalloc(&d, t.bytes) != hipSuccess) {
+    snprintf(msg, sizeof msg, "gguf: cannot allocate %llu bytes of device memory for %s", (unsigned long long)t.bytes, what);
+    return llb_fail_msg(LLB_HIP_EDEVICE, msg);
+  }
+  const uint64_t CH = 64ull << 20;
+  void* buf = nullptr;
+  if (hipHostMalloc(&buf, CH, 0) != hipSuccess) {
+    (void)hipFree(d);
+    return llb_fail_msg(LLB_HIP_EDEVICE, "gguf: cannot pin the upload buffer");
+  }
+  int rc = 0;
+  for (uint64_t k = 0; k < t.bytes && !rc; k += CH) {
+    const uint64_t c = t.bytes - k < CH ? t.bytes - k : CH;
+    for (uint64_t q = 0; q < c;) {
+      const ssize_t r = pread(g->fd, (uint8_t*)buf + q, (size_t)(c - q), (off_t)(t.off + k + q));
+      if (r <= 0) {
+        rc = llb_fail_msg(LLB_HIP_EINVAL, "gguf: read failed");
+        break;
+      }
+      q += (uint64_t)r;
+    }
+    if (!rc && hipMemcpy((uint8_t*)d + k, buf, c, hipMemcpyHostToDevice) != hipSuccess)
+      rc = llb_fail_msg(LLB_HIP_EDEVICE, "gguf: cannot upload a stack");
+  }
+  (void)hipHostFree(buf);
+  if (rc) {
+    (void)hipFree(d);
+    return rc;
+  }
+  *out = (llb_dptr)(uintptr_t)d;
+  return 0;
+}
+
+static void free_stack(int mode, llb_dptr p) {
+  if (!p) return;
+  if (mode == LLB_MOE_RES_HOST) {
+    hipPointerAttribute_t a;
+    void* h = (hipPointerGetAttributes(&a, (void*)(uintptr_t)p) == hipSuccess && a.hostPointer) ? a.hostPointer
+                                                                                            : (void*)(uintptr_t)p;
+    (void)hipHostFree(h);
+  } else {
+    (void)hipFree((void*)(uintptr_t)p);
+  }
+}
+
+// a named tensor of the layer with its expected format and bytes (the reference's check against the
+// sidecar, host/llb_host.c:509-515)
+static const GgTensor* want(const llb_gguf* g, uint32_t layer, const char* nm, uint32_t fm, uint64_t bytes, int* rc) {
+  char name[96], msg[256];
+  snprintf(name, sizeof name, "blk.%u.%s.weight", layer, nm);
+  const int i = llb_gguf_find(g, name);
+  if (i < 0) {
+    snprintf(msg, sizeof msg, "gguf: %s not found", name);
+    *rc = llb_fail_msg(LLB_HIP_EINVAL, msg);
+    return nullptr;
+  }
+  const GgTensor& t = g->t[(size_t)i];
+  if (gg_fm(t.type) != (int)fm || t.bytes != bytes) {
+    snprintf(msg, sizeof msg, "gguf: %s: ggml type %u, %llu bytes; the layer says format %u, %llu bytes", name, t.type,
+             (unsigned long long)t.bytes, fm, (unsigned long long)bytes);
+    *rc = llb_fail_msg(LLB_HIP_EINVAL, msg);
+    return nullptr;
+  }
+  return &t;
+}
+
+// per-layer stream state: the mapped file and the staging for k experts (llb_moe_load's mode 2)
+struct StreamSrc {
+  const uint8_t* map;
+  uint64_t map_bytes;
+  uint64_t sg, su, sd;  // stack offsets in the file
+  uint64_t esg, esd;    // expert strides of the gate (and up) and down stacks
+  bool fused;
+  void* pin;            // pinned host staging, nk experts
+  void* dev;            // device staging: nk gate (+ up) experts, then nk down experts
+  uint32_t* slots;      // device [nk] = 0 .. nk - 1: the ids the expert kernels see
+  uint32_t nk;
+};
+
+extern "C" {
+
+int llb_moe_hip_load_layer(llb_gguf* g, uint32_t layer, int mode, llb_moe_layer* L) {
+  if (!g || !L) return llb_fail_msg(LLB_HIP_EINVAL, "load: null file or layer");
+  if (mode < LLB_MOE_RES_DEVICE || mode > LLB_MOE_RES_STREAM) return llb_fail_msg(LLB_HIP_EINVAL, "load: no such mode");
+  const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
+  const uint64_t rbg = row_bytes(fg, L->dm), rbu = row_bytes(fu, L->dm), rbd = row_bytes(fd, L->ef);
+  if (!L->dm || !L->ne || !L->ef || !L->nk || !rbg || !rbu || !rbd) return llb_fail_msg(LLB_HIP_EINVAL, "load: the layer's shape words are not set");
+  int rc = 0;
+  const GgTensor* tg = want(g, layer, fz ? "ffn_gate_up_exps" : "ffn_gate_exps", fg,
+                            (uint64_t)L->ne * (fz ? 2 : 1) * L->ef * rbg, &rc);
+  if (!tg) return rc;
+  const GgTensor* tu = nullptr;
+  if (!fz && !(tu = want(g, layer, "ffn_up_exps", fu, (uint64_t)L->ne * L->ef * rbu, &rc))) return rc;
+  const GgTensor* td = want(g, layer, "ffn_down_exps", fd, (uint64_t)L->ne * L->dm * rbd, &rc);
+  if (!td) return rc;
+  // router, shared gate row and shared expert, when the caller has not placed them
+  struct Opt {
+    const char* nm;
+    llb_dptr* dst;
+    uint32_t fm;
+    uint64_t bytes;
+  } opt[5] = {
+      {"ffn_gate_inp", &L->router, LLB_FM_F32, (uint64_t)L->ne * L->dm * 4},
+      {"ffn_gate_inp_shexp", &L->shgate, LLB_FM_F32, (uint64_t)L->dm * 4},
+      {"ffn_gate_shexp", &L->SG, L->fsg, (uint64_t)L->sf * row_bytes(L->fsg, L->dm)},
+      {"ffn_up_shexp", &L->SU, L->fsu, (uint64_t)L->sf * row_bytes(L->fsu, L->dm)},
+      {"ffn_down_shexp", &L->SD, L->fsd, (uint64_t)L->dm * row_bytes(L->fsd, L->sf)},
+  };
+  const GgTensor* ot[5] = {};
+  for (int i = 0; i < 5; i++) {
+    if (*opt[i].dst || (i >= 1 && !L->sf)) continue;
+    char name[96];
+    snprintf(name, sizeof name, "blk.%u.%s.weight", layer, opt[i].nm);
+    if (llb_gguf_find(g, name) < 0) continue;  // the caller supplies it
+    if (!(ot[i] = want(g, layer, opt[i].nm, opt[i].fm, opt[i].bytes, &rc))) return rc;
+  }
+  llb_dptr got[3] = {0, 0, 0};
+  const GgTensor* st[3] = {tg, tu, td};
+  if (mode == LLB_MOE_RES_STREAM) {
+    struct stat sb;
+    if (fstat(g->fd, &sb) != 0) return llb_fail_msg(LLB_HIP_EINVAL, "load: cannot stat the file");
+    void* map = mmap(nullptr, (size_t)sb.st_size, PROT_READ, MAP_SHARED, g->fd, 0);
+    if (map == MAP_FAILED) return llb_fail_msg(LLB_HIP_EINVAL, "load: cannot map the file");
+    auto* s = new StreamSrc{};
+    s->map = (const uint8_t*)map;
+    s->map_bytes = (uint64_t)sb.st_size;
+    s->sg = tg->off;
+    s->su = tu ? tu->off : tg->off + (uint64_t)L->ef * rbg;
+    s->sd = td->off;
+    s->fused = fz;
+    s->esg = (uint64_t)(fz ? 2 : 1) * L->ef * rbg;
+    s->esd = (uint64_t)L->dm * rbd;
+    s->nk = L->nk;
+    const uint64_t ex = (fz ? s->esg : 2 * (uint64_t)L->ef * rbg) + s->esd;  // one expert's bytes
+    std::vector<uint32_t> sl(L->nk);
+    for (uint32_t j = 0; j < L->nk; j++) sl[j] = j;
+    if (hipHostMalloc(&s->pin, ex * L->nk, 0) != hipSuccess || hipMalloc(&s->dev, ex * L->nk) != hipSuccess ||
+        hipMalloc((void**)&s->slots, 4ull * L->nk) != hipSuccess ||
+        hipMemcpy(s->slots, sl.data(), 4ull * L->nk, hipMemcpyHostToDevice) != hipSuccess) {
+      if (s->pin) (void)hipHostFree(s->pin);
+      if (s->dev) (void)hipFree(s->dev);
+      if (s->slots) (void)hipFree(s->slots);
+      munmap(map, (size_t)sb.st_size);
+      delete s;
+      return llb_fail_msg(LLB_HIP_EDEVICE, "load: cannot allocate the stream staging");
+    }
+    L->stream = (llb_dptr)(uintptr_t)s;
+    // G / U / D: the device staging slots (gate of slot j at j esg-with-up-or-not, see the forward)
+    const uint64_t gb = fz ? s->esg : (uint64_t)L->ef * rbg;
+    got[0] = (llb_dptr)(uintptr_t)s->dev;
+    got[1] = fz ? 0 : got[0] + gb * L->nk;
+    got[2] = got[0] + (fz ? s->esg : 2 * gb) * L->nk;
+  } else {
+    for (int i = 0; i < 3; i++)
+      if (st[i] && (rc = fill(g, *st[i], mode, &got[i], i == 0 ? "a gate stack" : i == 1 ? "an up stack" : "a down stack"))) {
+        for (int k = 0; k < i; k++) free_stack(mode, got[k]);
+        return rc;
+      }
+  }
+  uint32_t own = 0;
+  for (int i = 0; i < 5; i++)
+    if (ot[i]) {
+      if ((rc = fill(g, *ot[i], LLB_MOE_RES_DEVICE, opt[i].dst, opt[i].nm))) return rc;
+      own |= 1u << i;
+    }
+  L->G = got[0];
+  L->U = fz ? 0 : got[1];
+  L->D = got[2];
+  L->res = (uint32_t)mode;
+  L->own = own;
+  return 0;
+}
+
+}  // extern "C"
+
+// the k chosen experts of one token into the device staging (the reference's per-token copy,
+// host/llb_host.c:680-696): ids read back, each expert's gate (+ up) and down bytes gathered from the
+// mapped file into pinned memory, then uploaded in order on the library stream. The slot ids 0..k-1
+// replace the experts' ids for the expert kernels.
+int stream_stage(const llb_moe_layer* L, const uint32_t* d_ids, const uint32_t** slots) {
+  auto* s = (StreamSrc*)(uintptr_t)L->stream;
+  if (!s) return llb_fail_msg(LLB_HIP_EINVAL, "stream: the layer has no stream source");
+  const hipStream_t st = llb_cur_stream();
+  std::vector<uint32_t> ids(s->nk);
+  if (hipMemcpyAsync(ids.data(), d_ids, 4ull * s->nk, hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess)
+    return llb_fail_msg(LLB_HIP_EDEVICE, "stream: cannot read the chosen experts back");
+  const uint64_t gb = s->esg, ub = s->fused ? 0 : s->esg, db = s->esd, ex = gb + ub + db;
+  uint8_t* pin = (uint8_t*)s->pin;
+  uint8_t* dev = (uint8_t*)s->dev;
+  for (uint32_t j = 0; j < s->nk; j++) {
+    const uint64_t e = ids[j];
+    if (e >= L->ne) return llb_fail_msg(LLB_HIP_EINVAL, "stream: an expert id out of range");
+    uint8_t* hp = pin + j * ex;
+    memcpy(hp, s->map + s->sg + e * s->esg, gb);
+    if (ub) memcpy(hp + gb, s->map + s->su + e * s->esg, ub);
+    memcpy(hp + gb + ub, s->map + s->sd + e * s->esd, db);
+    // device: gate slots [0, nk gb), up slots [nk gb, nk (gb + ub)), down slots after
+    if (hipMemcpyAsync(dev + j * gb, hp, gb, hipMemcpyHostToDevice, st) != hipSuccess ||
+        (ub && hipMemcpyAsync(dev + s->nk * gb + j * ub, hp + gb, ub, hipMemcpyHostToDevice, st) != hipSuccess) ||
+        hipMemcpyAsync(dev + s->nk * (gb + ub) + j * db, hp + gb + ub, db, hipMemcpyHostToDevice, st) != hipSuccess)
+      return llb_fail_msg(LLB_HIP_EDEVICE, "stream: cannot stage an expert");
+  }
+  *slots = s->slots;
+  return 0;
+}
+// the pinned staging is reused by the next token: wait for this token's uploads (the caller, after
+// the expert kernels are queued)
+int stream_done() {
+  return hipStreamSynchronize(llb_cur_stream()) == hipSuccess ? 0 : llb_fail_msg(LLB_HIP_EDEVICE, "stream: sync");
+}
+
+extern "C" int llb_moe_hip_unload_layer(llb_moe_layer* L) {
+  if (!L) return llb_fail_msg(LLB_HIP_EINVAL, "unload: null layer");
+  if (L->res == LLB_MOE_RES_STREAM) {
+    auto* s = (StreamSrc*)(uintptr_t)L->stream;
+    if (s) {
+      (void)hipStreamSynchronize(llb_cur_stream());
+      (void)hipHostFree(s->pin);
+      (void)hipFree(s->dev);
+      (void)hipFree(s->slots);
+      munmap((void*)s->map, (size_t)s->map_bytes);
+      delete s;
+    }
+    L->stream = 0;
+  } else {
+    free_stack((int)L->res, L->G);
+    free_stack((int)L->res, L->U);
+    free_stack((int)L->res, L->D);
+  }
+  llb_dptr* opt[5] = {&L->router, &L->shgate, &L->SG, &L->SU, &L->SD};
+  for (int i = 0; i < 5; i++)
+    if (L->own >> i & 1) {
+      free_stack(LLB_MOE_RES_DEVICE, *opt[i]);
+      *opt[i] = 0;
+    }
+  L->own = 0;
+  L->G = L->U = L->D = 0;
+  return 0;
+}

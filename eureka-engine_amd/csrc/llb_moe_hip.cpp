@@ -34,6 +34,9 @@ static int hip_ok(hipError_t e, const char* what) {
   if (e == hipSuccess) return 0;
   return fail(LLB_HIP_EDEVICE, "%s: %s", what, hipGetErrorString(e));
 }
+// for the library's other host files: set the error text, read the stream
+int llb_fail_msg(int code, const char* msg) { return fail(code, "%s", msg); }
+hipStream_t llb_cur_stream() { return g_stream; }
 // a launch's error (bad configuration, no device) is what hipGetLastError reports right after it
 static int launched(int rc, const char* what) {
   if (rc != 0) return fail(LLB_HIP_EINVAL, "%s: no kernel for this format / shape", what);
@@ -103,7 +106,11 @@ static void stage_collect() {
 
 template <class T> static T* dp(llb_dptr p) { return reinterpret_cast<T*>((uintptr_t)p); }
 
-static uint64_t row_bytes(uint32_t fm, uint32_t cols) {
+uint64_t llb_row_bytes(uint32_t fm, uint32_t cols);
+// stream residency (llb_moe_gguf.cpp): the token's k experts into the staging slots; *slots = their ids
+int stream_stage(const llb_moe_layer* L, const uint32_t* d_ids, const uint32_t** slots);
+static uint64_t row_bytes(uint32_t fm, uint32_t cols) { return llb_row_bytes(fm, cols); }
+uint64_t llb_row_bytes(uint32_t fm, uint32_t cols) {
   switch (fm) {
     case LLB_FM_F32: return (uint64_t)cols * 4;
     case LLB_FM_Q8_0: return (uint64_t)cols / 32 * 34;
@@ -531,8 +538,12 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
     return gemm_forward(L, T, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt), sc, s);
   // one token: the exact tier routes inside its gate / up launch (one launch fewer a layer; every
   // block recomputes the token's routing, which only pays off for a single token)
+  // stream residency (the k chosen experts copied in per token): exact tier, one token, eager
+  const bool streamed = L->res == LLB_MOE_RES_STREAM;
+  if (streamed && (tier != LLB_MOE_EXACT || T != 1 || g_capturing))
+    return fail(LLB_HIP_EINVAL, "stream residency: the exact tier, one token, outside graph capture");
   TopkArgs tk{};
-  const bool fuse_topk = tier == LLB_MOE_EXACT && fg == fu && T == 1;
+  const bool fuse_topk = tier == LLB_MOE_EXACT && fg == fu && T == 1 && !streamed;
   if ((rc = route(L, T, dp<float>(h2), dp<uint32_t>(ids), dp<float>(wt), sc, s, true, fuse_topk ? &tk : nullptr)))
     return rc;
   const uint64_t rbg = row_bytes(fg, L->dm), rbu = row_bytes(fu, L->dm);
@@ -557,6 +568,11 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
   g.ids = dp<uint32_t>(ids);
   g.act = (float*)(sc + s.act);
   g.es = esg;
+  if (streamed) {  // G / U / D are the staging slots, the experts' ids the slot numbers
+    const uint32_t* slots = nullptr;
+    if ((rc = stream_stage(L, dp<uint32_t>(ids), &slots))) return rc;
+    g.ids = slots;
+  }
   stage_begin(ST_GU);
   rc = fuse_topk ? launch_gu_topk(g, tk, fg, fu, T * L->nk, g_stream) : launch_gu_exact(g, fg, fu, T * L->nk, g_stream);
   if ((rc = launched(rc, fuse_topk ? "top-k + expert gate/up" : "expert gate/up"))) return rc;
@@ -581,6 +597,7 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
   stage_begin(ST_DN);
   rc = launched(launch_dn_exact(d, fd, L->sf ? L->fsd : 0, T, g_stream), "expert down + combine");
   stage_end(ST_DN);
+  if (!rc && streamed) rc = stream_done();
   return rc;
 }
 

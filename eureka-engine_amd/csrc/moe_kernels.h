@@ -124,6 +124,10 @@ struct GemmArgs {
 };
 int launch_moe_gemm(const GemmArgs& g, uint32_t fm, uint32_t mode, uint32_t grid_y, hipStream_t st);
 uint32_t gemm_bm();
+int llb_fail_msg(int code, const char* msg);  // sets llb_hip_last_error's text, returns code
+hipStream_t llb_cur_stream();
+// stream residency (llb_moe_gguf.cpp): stage_done waits for a token's uploads (the staging is reused)
+int stream_done();
 int launch_rmsnorm_add(const float* x, const float* z, const float* w, float eps, uint32_t T, uint32_t n, float* x1,
                        float* h2, hipStream_t st);
 uint64_t pack_bytes(uint32_t fm, uint32_t R, uint32_t K);

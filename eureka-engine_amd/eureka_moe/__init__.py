@@ -40,7 +40,8 @@ class MoeLayer(C.Structure):
                 ("router", C.c_uint64), ("shgate", C.c_uint64), ("G", C.c_uint64), ("U", C.c_uint64), ("D", C.c_uint64),
                 ("SG", C.c_uint64), ("SU", C.c_uint64), ("SD", C.c_uint64), ("router_bias", C.c_uint64),
                 ("PG", C.c_uint64), ("PU", C.c_uint64), ("PD", C.c_uint64),
-                ("PSG", C.c_uint64), ("PSU", C.c_uint64), ("PSD", C.c_uint64)]
+                ("PSG", C.c_uint64), ("PSU", C.c_uint64), ("PSD", C.c_uint64),
+                ("res", C.c_uint32), ("own", C.c_uint32), ("stream", C.c_uint64)]
 
 
 _SIGS = {
@@ -70,6 +71,15 @@ _SIGS = {
                                       C.c_uint64, C.c_uint64, C.c_size_t, C.c_int]),
     "llb_moe_hip_set_fused": (C.c_int, [C.c_int]),
     "llb_moe_hip_pack_bytes": (C.c_size_t, [C.POINTER(MoeLayer)]),
+    "llb_gguf_open": (C.c_void_p, [C.c_char_p]),
+    "llb_gguf_close": (None, [C.c_void_p]),
+    "llb_gguf_count": (C.c_uint64, [C.c_void_p]),
+    "llb_gguf_find": (C.c_int, [C.c_void_p, C.c_char_p]),
+    "llb_gguf_tensor_at": (C.c_int, [C.c_void_p, C.c_uint64, C.c_char_p, C.c_size_t, C.POINTER(C.c_uint64),
+                                     C.POINTER(C.c_uint64), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
+                                     C.POINTER(C.c_uint64)]),
+    "llb_moe_hip_load_layer": (C.c_int, [C.c_void_p, C.c_uint32, C.c_int, C.POINTER(MoeLayer)]),
+    "llb_moe_hip_unload_layer": (C.c_int, [C.POINTER(MoeLayer)]),
     "llb_moe_hip_pack": (C.c_int, [C.POINTER(MoeLayer), C.c_uint64, C.c_size_t]),
     "llb_moe_hip_status": (C.c_int, [C.c_uint64, C.POINTER(MoeLayer), C.c_uint32]),
     "llb_moe_hip_topk": (C.c_int, [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64,

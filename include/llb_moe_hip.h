@@ -83,6 +83,9 @@ typedef struct {
                          * reference: the batched-decode workload skews expert load with it */
   llb_dptr PG, PU, PD;    /* packed copies of G, U, D for the f16 tier (llb_moe_hip_pack; 0: none) */
   llb_dptr PSG, PSU, PSD; /* packed copies of SG, SU, SD */
+  uint32_t res;           /* residency of G / U / D (LLB_MOE_RES_*; 0 = device, the default) */
+  uint32_t own;           /* router, shgate, SG, SU, SD (bits 0..4) that llb_moe_hip_load_layer allocated */
+  llb_dptr stream;        /* LLB_MOE_RES_STREAM: the loader's per-layer source (host address; 0 otherwise) */
 } llb_moe_layer;
 
 /* ---- the layer's table row (host code) ----
@@ -116,6 +119,30 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
  * launch on that scratch had a bounded wait time out. No counterpart in the reference. */
 int llb_moe_hip_set_fused(int on);
 int llb_moe_hip_status(llb_dptr scratch, const llb_moe_layer* L, uint32_t T);
+
+/* ---- GGUF expert stacks: llb_moe_load's residency (host/llb_host.c:446-586) and llb_gg_tensor
+ * (host/llb_gguf.c:854-865). open parses a GGUF (v2 / v3) header, every length checked against the
+ * file; find returns a tensor's index or -1; tensor_at its name, absolute file offset, bytes (0 for a
+ * type this path does not read), ggml type and dims (ne[0] fastest). load_layer fills L->G / U / D for
+ * blk.<layer>.ffn_{gate,up,down}_exps (ffn_gate_up_exps when fx bit 12 is set) after checking each
+ * tensor's type and bytes against L's formats and shape words, and also router / shgate / SG / SU / SD
+ * from ffn_gate_inp, ffn_gate_inp_shexp and ffn_{gate,up,down}_shexp when the file holds them and L
+ * does not already point at them. Modes: DEVICE (device memory), HOST (pinned, device-mapped host
+ * memory; the kernels read it over the bus), STREAM (the file mapped; llb_moe_hip_forward copies the k
+ * chosen experts of each token into device staging slots -- exact tier, one token, no graph capture).
+ * Every mode gives the same bits. unload_layer frees what load_layer allocated. */
+#define LLB_MOE_RES_DEVICE 0
+#define LLB_MOE_RES_HOST 1
+#define LLB_MOE_RES_STREAM 2
+typedef struct llb_gguf llb_gguf;
+llb_gguf* llb_gguf_open(const char* path);
+void llb_gguf_close(llb_gguf* g);
+uint64_t llb_gguf_count(const llb_gguf* g);
+int llb_gguf_find(const llb_gguf* g, const char* name);
+int llb_gguf_tensor_at(const llb_gguf* g, uint64_t i, char* name, size_t cap, uint64_t* offset, uint64_t* bytes,
+                       uint32_t* type, uint32_t* nd, uint64_t* dims);
+int llb_moe_hip_load_layer(llb_gguf* g, uint32_t layer, int mode, llb_moe_layer* L);
+int llb_moe_hip_unload_layer(llb_moe_layer* L);
 
 /* ---- packed weights for the f16 tier. No counterpart in the reference, whose prefill decodes GGUF
  * blocks where they lie. The grouped GEMM reads each weight tile of 32 rows x 64 columns as one

@@ -417,3 +417,51 @@ def test_rmsnorm_add_bit_exact(dev, n):
     rx1, rh2, _ = ol.rmsnorm_add(x, z, w, eps)
     assert np.array_equal(x1.view(np.uint32), rx1.view(np.uint32))
     assert np.array_equal(h2.view(np.uint32), rh2.view(np.uint32)), np.abs(h2 - rh2).max()
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2])
+def test_gguf_load_same_bits_every_mode(dev, tmp_path, mode):
+    """GGUF expert stacks (llb_moe_load's residency, host/llb_host.c:446-586) in device, host-mapped and
+    stream mode: the stacks' bytes are the generator's, and decode gives the same ids, weights and y bits
+    as the device-generated layer in every mode (the reference's same-bits gate across its modes)"""
+    import gguf_io
+    shape = SMALL[0]
+    _say("gguf load mode", mode)
+    path = str(tmp_path / "layer.gguf")
+    gguf_io.write(path, gguf_io.layer_tensors(shape, seed=11, layer=0))
+    g = dev.lib.llb_gguf_open(path.encode())
+    assert g, dev.lib.llb_hip_last_error()
+    s = shape
+    desc = em.MoeLayer(s.dm, s.ne, s.nk, s.ef, s.sf, s.fx, s.fsg, s.fsu, s.fsd)
+    dev.check(dev.lib.llb_moe_hip_load_layer(g, 0, mode, C.byref(desc)))
+    ref = em.Layer(dev, shape, seed=11)
+    try:
+        assert desc.own == 0b11111  # router, shared gate row and shared expert came from the file
+        if mode != 2:
+            gb, ub, db = s.stack_bytes()
+            for a, b, n in ((desc.G, ref.G, gb), (desc.U, ref.U, ub), (desc.D, ref.D, db), (desc.router, ref.router, s.ne * s.dm * 4)):
+                assert np.array_equal(dev.read(a, (n,), np.uint8), dev.read(b, (n,), np.uint8))
+
+        class Loaded:
+            pass
+        lo = Loaded()
+        lo.desc = desc
+        run = em.Runner(dev, shape, 1, tier=em.EXACT)
+        for t in range(4):
+            run.gen_inputs(seed=20 + t)
+            run.forward(ref)
+            y0, i0, w0 = run.outputs()
+            run.forward(lo)
+            y1, i1, w1 = run.outputs()
+            assert np.array_equal(i0, i1) and np.array_equal(w0.view(np.uint32), w1.view(np.uint32))
+            assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32))
+        run.free()
+        if mode == 2:  # streaming is one token of the exact tier
+            r2 = em.Runner(dev, shape, 2, tier=em.EXACT)
+            assert dev.lib.llb_moe_hip_forward(C.byref(desc), 2, r2.h2, r2.x1, r2.y, r2.ids, r2.wt, r2.scratch,
+                                               r2.scratch_bytes, em.EXACT) != 0
+            r2.free()
+    finally:
+        ref.free()
+        dev.check(dev.lib.llb_moe_hip_unload_layer(C.byref(desc)))
+        dev.lib.llb_gguf_close(g)
