@@ -7,7 +7,7 @@ top-8, expert ff 512, shared expert 512, gate/up Q4_K, down Q6_K -- decoding one
 A step = one token through the 40 layers; value = microseconds per token-layer.
 
   python bench.py [--steps K] [--warmup W] [--layers L] [--config c2] [--tier exact|q8] [--no-cpu]
-                  [--legs batched,prefill,prefill_k,c5,rmsnorm]
+                  [--legs batched,prefill,prefill_k,c5,rmsnorm,residency]
   python bench.py --copy-calib          (the PMC byte-counter calibration copies only)
   python bench.py --traffic-from DIR    (profiles/traffic.json from rocprofv3 FETCH_SIZE / WRITE_SIZE passes)
 """
@@ -213,6 +213,63 @@ def rmsnorm_leg(dev, n, steps=50):
     return out
 
 
+def residency_leg(dev, shape, tokens=16):
+    """GGUF expert stacks (llb_moe_hip_load_layer) in each residency mode on one layer of `shape`: the
+    file is written from a device-generated layer (the same bytes), then per mode the load time (file to
+    placement: GB/s of expert stacks) and eager exact-tier decode microseconds a token-layer."""
+    import tempfile
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import gguf_io
+    s = shape
+    L = em.Layer(dev, s, seed=6, layer=0)
+    gb, ub, db = s.stack_bytes()
+    rd = lambda p, n: dev.read(p, (n,), np.uint8).tobytes()  # noqa: E731
+    ts = [("blk.0.ffn_gate_inp.weight", 0, (s.dm, s.ne), rd(L.router, s.ne * s.dm * 4)),
+          ("blk.0.ffn_gate_exps.weight", gguf_io.GGML[s.fg], (s.dm, s.ef, s.ne), rd(L.G, gb)),
+          ("blk.0.ffn_up_exps.weight", gguf_io.GGML[s.fu], (s.dm, s.ef, s.ne), rd(L.U, ub)),
+          ("blk.0.ffn_down_exps.weight", gguf_io.GGML[s.fd], (s.ef, s.dm, s.ne), rd(L.D, db))]
+    if s.sf:
+        ts += [("blk.0.ffn_gate_inp_shexp.weight", 0, (s.dm,), rd(L.shgate, s.dm * 4)),
+               ("blk.0.ffn_gate_shexp.weight", gguf_io.GGML[s.fsg], (s.dm, s.sf), rd(L.SG, s.sf * em.row_bytes(s.fsg, s.dm))),
+               ("blk.0.ffn_up_shexp.weight", gguf_io.GGML[s.fsu], (s.dm, s.sf), rd(L.SU, s.sf * em.row_bytes(s.fsu, s.dm))),
+               ("blk.0.ffn_down_shexp.weight", gguf_io.GGML[s.fsd], (s.sf, s.dm), rd(L.SD, s.dm * em.row_bytes(s.fsd, s.sf)))]
+    L.free()
+    out = {}
+    with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as td:
+        path = os.path.join(td, "layer.gguf")
+        gguf_io.write(path, ts)
+        g = dev.lib.llb_gguf_open(path.encode())
+        assert g, dev.lib.llb_hip_last_error()
+        run = em.Runner(dev, s, 1, tier=em.EXACT)
+        for mode, name in ((0, "device"), (1, "host"), (2, "stream")):
+            desc = em.MoeLayer(s.dm, s.ne, s.nk, s.ef, s.sf, s.fx, s.fsg, s.fsu, s.fsd)
+            t0 = time.perf_counter()
+            dev.check(dev.lib.llb_moe_hip_load_layer(g, 0, mode, C.byref(desc)))
+            dev.sync()
+            load_s = time.perf_counter() - t0
+
+            class Lo:
+                pass
+            lo = Lo()
+            lo.desc = desc
+            run.gen_inputs(7)
+            run.forward(lo)
+            dev.sync()
+            t0 = time.perf_counter()
+            for _ in range(tokens):
+                run.forward(lo)
+            dev.sync()
+            us = (time.perf_counter() - t0) / tokens * 1e6
+            dev.check(dev.lib.llb_moe_hip_unload_layer(C.byref(desc)))
+            out[name] = {"load_s": round(load_s, 3), "load_gbs": round((gb + ub + db) / load_s / 1e9, 2),
+                         "decode_us_per_token_layer": round(us, 1)}
+        run.free()
+        dev.lib.llb_gguf_close(g)
+    out["config"] = (f"one {s.ne}-expert layer ({(gb + ub + db) / 1e9:.2f} GB of expert stacks) from a GGUF on the "
+                     f"box's local disk (page cache warm after the write); eager exact-tier decode, {tokens} tokens")
+    return out
+
+
 def cpu_baseline(shape, seconds=12.0):
     """the CPU oracle's exact layer, single thread, on tokens of layer 0 (experts generated first)."""
     import oracle_lib as ol
@@ -251,8 +308,9 @@ def main():
     ap.add_argument("--prefill-T", type=int, default=2048)
     ap.add_argument("--no-c5", dest="c5", action="store_false",
                     help="skip the config-5 leg (48 resident 512-expert layers, 1 + 512 tokens a launch)")
-    ap.add_argument("--legs", default="batched,prefill,prefill_k,c5,rmsnorm",
-                    help="legs after the decode line: batched (config 3), prefill (c1), prefill_k (c1k), c5, rmsnorm")
+    ap.add_argument("--legs", default="batched,prefill,prefill_k,c5,rmsnorm,residency",
+                    help="legs after the decode line: batched (config 3), prefill (c1), prefill_k (c1k), c5, "
+                         "rmsnorm, residency (GGUF stacks in each residency mode)")
     ap.add_argument("--traffic-from", metavar="DIR",
                     help="only write profiles/traffic.json from the PMC csv directories under DIR and exit")
     ap.add_argument("--copy-calib", action="store_true",
@@ -378,6 +436,8 @@ def main():
         c5["tokens_per_s"] = round(513 / (c5["us_per_layer"] * 1e-6), 1)
         c5["config"] = "c5: 48 layers x 512 experts top-10 (Q4_K gate/up, Q6_K down, shared expert), 1 + 512 tokens a launch, f16 tier, packed stacks"
         out["c5_mixed"] = c5
+    if "residency" in legs:
+        out["residency_gguf"] = residency_leg(dev, shape)
     if "rmsnorm" in legs:
         out["rmsnorm_add"] = rmsnorm_leg(dev, shape.dm)
     if not args.no_cpu:
