@@ -151,9 +151,10 @@ __global__ void __launch_bounds__(64) k_tree_rows(TreeArgs a) {
   BSTAMP(0, 1);
 }
 
-// Many tokens (prefill, batches): a block of four waves takes 8 consecutive rows and tiles of TT tokens.
-// A tile's x rows are staged in LDS once (coalesced loads, lanes padded 4 floats apart); each wave holds
-// its two rows' weights in registers (lane L: the contiguous leaves [NQ L, NQ L + NQ)) and reduces
+// Many tokens (prefill, batches): a block of four waves takes 4 RW consecutive rows (RW = 4 for rows of
+// one span a lane, 2 for two) and tiles of TT tokens. A tile's x rows are staged in LDS once (coalesced
+// loads, lanes padded 4 floats apart), each token's x read from LDS once for a wave's RW rows; each wave
+// holds its rows' weights in registers (lane L: the contiguous leaves [NQ L, NQ L + NQ)) and reduces
 // them against every token: the in-lane levels, then tree64_asc -- the same tree as tree_body, so the
 // same sums.
 // A block walks `ntb` consecutive tiles of TT tokens (grid.y = ceil(T / (TT ntb))) with its rows'
@@ -162,33 +163,34 @@ __global__ void __launch_bounds__(64) k_tree_rows(TreeArgs a) {
 // the segment table and the row pointers come through scalar loads, ahead of every vector load.
 template <u32 NSP, u32 TT>
 DEV void tree_mt_load_x(const TreeArgs& a, u32 tid, u32 t0, float4* xl) {
-  constexpr u32 NQ = 8 * NSP;
+  constexpr u32 NQ = 8 * NSP, XJ = TT * 64 * NQ / 256;
   const u32 nl4 = a.cols / 4;
 #pragma unroll
-  for (u32 j = 0; j < 16; j++) {  // tokens past T and columns past cols are zeros
+  for (u32 j = 0; j < XJ; j++) {  // tokens past T and columns past cols are zeros
     const u32 i = tid + 256 * j, tt = i / (64 * NQ), li = i % (64 * NQ), t = t0 + tt;
     xl[j] = (t < a.T && li < nl4) ? ((const float4*)(a.x + (u64)t * a.xstride))[li] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
 }
-template <u32 NSP, u32 TT>
+template <u32 NSP, u32 TT, u32 RW>
 __global__ void __launch_bounds__(256) k_tree_rows_mt(TreeArgs a, u32 ntb) {
   constexpr u32 NQ = 8 * NSP, LS = 4 * NQ + 4;
-  static_assert(TT * 64 * NQ == 16 * 256, "sixteen float4 a thread");
+  constexpr u32 XJ = TT * 64 * NQ / 256;  // float4 staging loads a thread
+  static_assert(XJ * 256 == TT * 64 * NQ, "whole float4s a thread");
   constexpr u32 LS4 = LS / 4;
   extern __shared__ float4 xsh4[];  // [TT][64 lanes][LS floats]
   const u32 tid = threadIdx.x, L = tid & 63;
   const u32 w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // this wave's two rows: segment, row in it, output and bias (wave-uniform)
+  // this wave's RW rows: segment, row in it, output and bias (wave-uniform)
   const u32 c0 = 32 * NSP * L;
   const bool live = c0 < a.cols;
-  const u8* wp[2];
-  float* op[2];
-  u32 fm[2], ost[2];
-  bool has[2], hb[2];
-  float bia[2];
+  const u8* wp[RW];
+  float* op[RW];
+  u32 fm[RW], ost[RW];
+  bool has[RW], hb[RW];
+  float bia[RW];
 #pragma unroll
-  for (u32 k = 0; k < 2; k++) {
-    u32 r = blockIdx.x * 8 + 2 * w + k, s = 0;
+  for (u32 k = 0; k < RW; k++) {
+    u32 r = blockIdx.x * 4 * RW + RW * w + k, s = 0;
     while (s < a.nseg && r >= a.seg[s].rows) { r -= a.seg[s].rows; s++; }
     has[k] = s < a.nseg;  // false: past the last row
     const TreeSeg& sg = a.seg[has[k] ? s : 0];
@@ -201,9 +203,9 @@ __global__ void __launch_bounds__(256) k_tree_rows_mt(TreeArgs a, u32 ntb) {
     has[k] = has[k] && sg.out != nullptr;
   }
   const u32 tb = blockIdx.y * TT * ntb;
-  float wr[2][32 * NSP];
+  float wr[RW][32 * NSP];
 #pragma unroll
-  for (u32 k = 0; k < 2; k++) {
+  for (u32 k = 0; k < RW; k++) {
     const bool ok = live && has[k];
 #pragma unroll
     for (u32 q = 0; q < NSP; q++) {
@@ -221,30 +223,30 @@ __global__ void __launch_bounds__(256) k_tree_rows_mt(TreeArgs a, u32 ntb) {
       }
     }
   }
-  float4 xl[16];
+  float4 xl[XJ];
   tree_mt_load_x<NSP, TT>(a, tid, tb, xl);
   for (u32 j = 0; j < ntb; j++) {
     const u32 t0 = tb + j * TT;
     if (t0 >= a.T) break;  // block-uniform
     if (j) __syncthreads();  // every wave is done with the previous tile's x
 #pragma unroll
-    for (u32 jj = 0; jj < 16; jj++) {
+    for (u32 jj = 0; jj < XJ; jj++) {
       const u32 i = tid + 256 * jj, tt = i / (64 * NQ), li = i % (64 * NQ);
       xsh4[tt * 64 * LS4 + (li / NQ) * LS4 + li % NQ] = xl[jj];
     }
     __syncthreads();
     if (j + 1 < ntb && t0 + TT < a.T) tree_mt_load_x<NSP, TT>(a, tid, t0 + TT, xl);  // next tile in flight
     // every token of the tile (rows past T are zeros, their sums never stored): the in-lane levels
-    // first, then the six cross-lane levels of all 2 TT sums together -- independent chains, so the
+    // first, then the six cross-lane levels of all RW TT sums together -- independent chains, so the
     // DPP and permlane latencies overlap -- and one store block
-    float v[TT][2];
+    float v[TT][RW];
 #pragma unroll
     for (u32 tt = 0; tt < TT; tt++) {
       float4 xv[NQ];
 #pragma unroll
       for (u32 q = 0; q < NQ; q++) xv[q] = xsh4[tt * 64 * LS4 + L * LS4 + q];
 #pragma unroll
-      for (u32 k = 0; k < 2; k++) {
+      for (u32 k = 0; k < RW; k++) {
         float n[NQ];
 #pragma unroll
         for (u32 q = 0; q < NQ; q++) n[q] = leaf4(wr[k] + 4 * q, xv[q]);
@@ -254,12 +256,12 @@ __global__ void __launch_bounds__(256) k_tree_rows_mt(TreeArgs a, u32 ntb) {
 #pragma unroll
     for (u32 tt = 0; tt < TT; tt++)
 #pragma unroll
-      for (u32 k = 0; k < 2; k++) v[tt][k] = tree64_asc(v[tt][k]);
+      for (u32 k = 0; k < RW; k++) v[tt][k] = tree64_asc(v[tt][k]);
     if (L == 0) {
 #pragma unroll
       for (u32 tt = 0; tt < TT; tt++)
 #pragma unroll
-        for (u32 k = 0; k < 2; k++)
+        for (u32 k = 0; k < RW; k++)
           if (has[k] && t0 + tt < a.T) op[k][(u64)(t0 + tt) * ost[k]] = hb[k] ? v[tt][k] + bia[k] : v[tt][k];
     }
   }
@@ -1116,12 +1118,12 @@ int launch_tree_rows(const TreeArgs& a, u32 nsp, hipStream_t st) {
   for (u32 i = 0; i < a.nseg; i++) rows += a.seg[i].rows;
   if (rows == 0) return 0;
   if (a.T >= 16 && nsp <= 2) {  // token tiles: weights read once a tile
-    const u32 tt = nsp == 1 ? 8u : 4u;
+    const u32 tt = 4, rw = nsp == 1 ? 4u : 2u;
     const size_t sm = (size_t)tt * 64 * (32 * nsp + 4) * 4;
     // tiles a block: the count that minimises (rounds of resident blocks) x (tiles a block + 2, a
     // block's own cost of loading its rows and filling its pipeline), two blocks resident a CU -- a
     // grid just past one round of blocks would otherwise take two
-    const u32 rb = (rows + 7) / 8, nt = (a.T + tt - 1) / tt, slots = 2 * cu_count();
+    const u32 rb = (rows + 4 * rw - 1) / (4 * rw), nt = (a.T + tt - 1) / tt, slots = 2 * cu_count();
     u32 ntb = 1;
     u64 best = ~0ull;
     for (u32 n = 1; n <= nt; n++) {
@@ -1131,11 +1133,11 @@ int launch_tree_rows(const TreeArgs& a, u32 nsp, hipStream_t st) {
     const dim3 grid(rb, (nt + ntb - 1) / ntb);
     static bool set1 = false, set2 = false;
     if (nsp == 1) {
-      if (!set1) { (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<1, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm); set1 = true; }
-      LAUNCH_K((k_tree_rows_mt<1, 8>), grid, dim3(256), sm, st, a, ntb);
+      if (!set1) { (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<1, 4, 4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm); set1 = true; }
+      LAUNCH_K((k_tree_rows_mt<1, 4, 4>), grid, dim3(256), sm, st, a, ntb);
     } else {
-      if (!set2) { (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<2, 4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm); set2 = true; }
-      LAUNCH_K((k_tree_rows_mt<2, 4>), grid, dim3(256), sm, st, a, ntb);
+      if (!set2) { (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<2, 4, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm); set2 = true; }
+      LAUNCH_K((k_tree_rows_mt<2, 4, 2>), grid, dim3(256), sm, st, a, ntb);
     }
     return 0;
   }

@@ -11,21 +11,23 @@ import pytest
 
 
 def launch(nsp, T, rows, cus=256):
-    """launch_tree_rows' choice for T >= 16, nsp <= 2: TT, dynamic LDS bytes, ntb, grid"""
-    tt = 8 if nsp == 1 else 4
+    """launch_tree_rows' choice for T >= 16, nsp <= 2: TT, dynamic LDS bytes, ntb, grid, rows a wave"""
+    tt, rw = 4, (4 if nsp == 1 else 2)
     sm = tt * 64 * (32 * nsp + 4) * 4
-    rb, nt, slots = (rows + 7) // 8, (T + tt - 1) // tt, 2 * cus
+    rb, nt, slots = (rows + 4 * rw - 1) // (4 * rw), (T + tt - 1) // tt, 2 * cus
     ntb, best = 1, None
     for n in range(1, nt + 1):
         cost = (rb * ((nt + n - 1) // n) + slots - 1) // slots * (n + 2)
         if best is None or cost < best:
             ntb, best = n, cost
-    return tt, sm, ntb, (rb, (nt + ntb - 1) // ntb)
+    return tt, sm, ntb, (rb, (nt + ntb - 1) // ntb), rw
 
 
 def test_tree_mt_tiles_a_block():
-    assert launch(1, 513, 513)[2] == 10   # config 5: 65 x 7 blocks in one round, not 65 x 9 in two
-    assert launch(1, 2048, 128)[2] == 8   # the 2048-token prefill: 16 x 32 blocks, one round
+    for T, rows in ((513, 513), (2048, 128), (64, 128), (2048, 257)):
+        TT, _, ntb, (gx, gy), _ = launch(1, T, rows)
+        assert gx * gy <= 512 or ntb == 1   # one round of resident blocks unless a tile a block
+        assert gy * ntb * TT >= T
 
 
 def check(nsp, cols, T, segrows, wfmt_bytes=4):
@@ -33,14 +35,16 @@ def check(nsp, cols, T, segrows, wfmt_bytes=4):
     LS4 = (4 * NQ + 4) // 4
     nl4 = cols // 4
     rows = sum(segrows)
-    TT, sm, ntb, (gx, gy) = launch(nsp, T, rows)
+    TT, sm, ntb, (gx, gy), RW = launch(nsp, T, rows)
     assert sm <= 160 * 1024
     lds4 = sm // 16
     tid = np.arange(256)
     L = tid & 63
     written = [np.zeros((T, r), np.int32) for r in segrows]
     # x staging: thread tid, load jj reads x row t0 + i / (64 NQ), float4 i % (64 NQ)
-    i = tid[:, None] + 256 * np.arange(16)[None, :]
+    XJ = TT * 64 * NQ // 256
+    assert XJ * 256 == TT * 64 * NQ
+    i = tid[:, None] + 256 * np.arange(XJ)[None, :]
     tts, li = i // (64 * NQ), i % (64 * NQ)
     st = tts * 64 * LS4 + (li // NQ) * LS4 + li % NQ
     assert st.min() >= 0 and st.max() < lds4
@@ -57,8 +61,8 @@ def check(nsp, cols, T, segrows, wfmt_bytes=4):
             assert (li[live] * 4 + 4 <= cols).all() and (t[live] < T).all()
         for bx in range(gx):
             for w in range(4):
-                for k in range(2):
-                    r, s = bx * 8 + 2 * w + k, 0
+                for k in range(RW):
+                    r, s = bx * 4 * RW + RW * w + k, 0
                     while s < len(segrows) and r >= segrows[s]:
                         r -= segrows[s]
                         s += 1
@@ -100,5 +104,6 @@ def test_tree_mt_grid_covers_tokens():
     for T in (16, 17, 63, 64, 513, 2047, 2048, 4096):
         for rows in (1, 8, 129, 513, 1024):
             for nsp in (1, 2):
-                TT, _, ntb, (gx, gy) = launch(nsp, T, rows, cus=(256, 80, 304)[(T + rows) % 3])
+                TT, _, ntb, (gx, gy), RW = launch(nsp, T, rows, cus=(256, 80, 304)[(T + rows) % 3])
+                assert gx * 4 * RW >= rows
                 assert gy * ntb * TT >= T and (gy - 1) * ntb * TT < T
