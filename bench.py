@@ -7,7 +7,7 @@ top-8, expert ff 512, shared expert 512, gate/up Q4_K, down Q6_K -- decoding one
 A step = one token through the 40 layers; value = microseconds per token-layer.
 
   python bench.py [--steps K] [--warmup W] [--layers L] [--config c2] [--tier exact|q8] [--no-cpu]
-                  [--legs batched,prefill,prefill_k,c5,rmsnorm,residency]
+                  [--legs q8,batched,prefill,prefill_k,c5,rmsnorm,residency]
   python bench.py --copy-calib          (the PMC byte-counter calibration copies only)
   python bench.py --traffic-from DIR    (profiles/traffic.json from rocprofv3 FETCH_SIZE / WRITE_SIZE passes)
 """
@@ -308,9 +308,9 @@ def main():
     ap.add_argument("--prefill-T", type=int, default=2048)
     ap.add_argument("--no-c5", dest="c5", action="store_false",
                     help="skip the config-5 leg (48 resident 512-expert layers, 1 + 512 tokens a launch)")
-    ap.add_argument("--legs", default="batched,prefill,prefill_k,c5,rmsnorm,residency",
-                    help="legs after the decode line: batched (config 3), prefill (c1), prefill_k (c1k), c5, "
-                         "rmsnorm, residency (GGUF stacks in each residency mode)")
+    ap.add_argument("--legs", default="q8,batched,prefill,prefill_k,c5,rmsnorm,residency",
+                    help="legs after the decode line: q8 (the int8 tier's decode), batched (config 3), prefill (c1), "
+                         "prefill_k (c1k), c5, rmsnorm, residency (GGUF stacks in each residency mode)")
     ap.add_argument("--traffic-from", metavar="DIR",
                     help="only write profiles/traffic.json from the PMC csv directories under DIR and exit")
     ap.add_argument("--copy-calib", action="store_true",
@@ -387,6 +387,31 @@ def main():
     stages = dev.timing_read()
     dev.timing(False)
 
+    # the int8 tier (expert products on q8_1 activations, llb_mx_*'s arithmetic) on the same layers and
+    # tokens, one graph a step
+    q8_us = None
+    if "q8" in legs and tier == em.EXACT:
+        def step_q8():
+            for i, L in enumerate(layers):
+                dev.check(dev.lib.llb_moe_hip_forward(C.byref(L.desc), T, h2 + i * shape.dm * 4, x1 + i * shape.dm * 4,
+                                                      y + i * shape.dm * 4, ids + i * shape.nk * 4, wt + i * shape.nk * 4,
+                                                      sc8, sb8, em.Q8))
+        sb8 = dev.lib.llb_moe_hip_scratch_bytes(C.byref(layers[0].desc), T, em.Q8)
+        sc8 = dev.alloc(sb8)
+        run8 = step_q8
+        if args.graph:
+            g8 = dev.capture(step_q8)
+            run8 = lambda: dev.replay(g8)  # noqa: E731
+        for _ in range(args.warmup):
+            run8()
+        dev.sync()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            run8()
+        dev.sync()
+        q8_us = (time.perf_counter() - t0) / (args.steps * args.layers) * 1e6
+        dev.free(sc8)
+
     sbytes = stage_bytes(shape)
     dom = max(("gate_up", "down"), key=lambda k: stages.get(k, (0, 0))[0])
     dom_us = stages[dom][0]
@@ -413,6 +438,10 @@ def main():
                      "traffic": measured_traffic(f"{args.config}_decode", dom, args.tier == "exact"),
                      "bytes_per_launch": sbytes[dom], "kernel_us": round(dom_us, 3)},
     }
+    if q8_us is not None:
+        out["decode_q8_tier"] = {"us_per_token_layer": round(q8_us, 3),
+                                 "config": f"{args.config} decode, the int8 tier (q8_1 activations, v_dot4), same layers "
+                                           f"and tokens{', one HIP graph a step' if args.graph else ''}"}
     if "batched" in legs:
         b3 = {}
         for tn, tv in (("f16", em.F16), ("exact", em.EXACT)):
