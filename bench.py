@@ -172,6 +172,12 @@ def batched(dev, shape, T, layers, steps, warmup, tier):
             run.forward(L)
     dev.sync()
     wall = time.perf_counter() - t0
+    dev.timing(1)
+    dev.check(dev.lib.llb_hip_spin(20000))
+    for L in Ls:
+        run.forward(L)
+    st = dev.timing_read()
+    dev.timing(False)
     ids = dev.read(run.ids, (T, shape.nk), np.uint32)
     uniq = int(np.unique(ids).size)
     run.free()
@@ -181,6 +187,7 @@ def batched(dev, shape, T, layers, steps, warmup, tier):
     byts = uniq * shape.expert_bytes() + shape.ne * shape.dm * 4 + shape.shared_bytes()
     return {"us_per_layer": round(us, 2), "us_per_token_layer": round(us / T, 3), "T": T,
             "unique_experts_last_layer": uniq, "algorithmic_bytes_last_layer": byts,
+            "stages_us": {k: round(v[0], 2) for k, v in st.items()},
             "hbm_frac_last_layer": round(byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 

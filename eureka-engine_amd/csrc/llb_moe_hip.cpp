@@ -16,7 +16,7 @@ int moe_q8_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const fl
                    const float* wt, const float* sgo, uint8_t* scratch, hipStream_t st);
 size_t moe_q8_scratch(const llb_moe_layer* L, uint32_t T);
 int launch_group(const uint32_t* ids, uint32_t n, uint32_t nk, uint32_t ne, uint32_t* off, uint32_t* xmap,
-                 uint32_t* inv, uint32_t* cnt, hipStream_t st);
+                 uint32_t* inv, const float* x, _Float16* x16, uint64_t nx, hipStream_t st);
 int launch_q8_1(const float* x, uint32_t n, int8_t* q, float2* ds, hipStream_t st);
 int launch_spin(uint32_t us, hipStream_t st);
 
@@ -262,7 +262,7 @@ static ExactScratch exact_layout(const llb_moe_layer* L, uint32_t T) {
 }
 
 struct GemmScratch {
-  size_t x16, off, xmap, inv, tiles, ntiles, act, out, sact, shd, total;
+  size_t x16, off, xmap, inv, act, out, sact, shd, total;
 };
 static GemmScratch gemm_layout(const llb_moe_layer* L, uint32_t T) {
   GemmScratch g;
@@ -272,8 +272,6 @@ static GemmScratch gemm_layout(const llb_moe_layer* L, uint32_t T) {
   g.off = o; o += al(((size_t)L->ne + 1) * 4);
   g.xmap = o; o += al(n * 4);
   g.inv = o; o += al(n * 4);
-  g.tiles = o; o += al((n / gemm_bm() + L->ne + 1) * 4);
-  g.ntiles = o; o += al(4);
   g.act = o; o += al(n * L->ef * 2);
   g.out = o; o += al(n * L->dm * 4);
   g.sact = o; o += al((size_t)T * L->sf * 2 + 4);
@@ -344,8 +342,8 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
   const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
   if (fg != fu) return fail(LLB_HIP_EINVAL, "f16 tier: gate and up in one format");
   if (L->sf && L->fsg != L->fsu) return fail(LLB_HIP_EINVAL, "f16 tier: shared gate and up in one format");
-  if (L->dm % 256 || L->ef % 128 || L->sf % 128 || L->ne >= 65536)
-    return fail(LLB_HIP_EINVAL, "f16 tier: dm a multiple of 256, ef and sf of 128");
+  if (L->dm % 256 || L->ef % 128 || L->sf % 128 || L->ne > 1024)
+    return fail(LLB_HIP_EINVAL, "f16 tier: dm a multiple of 256, ef and sf of 128, at most 1024 experts");
   const GemmScratch gs = gemm_layout(L, T);
   uint8_t* gb = sc + s.total;
   int rc;
@@ -354,13 +352,11 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
   uint32_t* off = (uint32_t*)(gb + gs.off);
   uint32_t* xmap = (uint32_t*)(gb + gs.xmap);
   uint32_t* inv = (uint32_t*)(gb + gs.inv);
-  uint32_t* tiles = (uint32_t*)(gb + gs.tiles);
-  uint32_t* ntiles = (uint32_t*)(gb + gs.ntiles);
   _Float16* x16 = (_Float16*)(gb + gs.x16);
   stage_begin(ST_Q8X);
-  if ((rc = launched(launch_group(ids, n, L->nk, L->ne, off, xmap, inv, nullptr, g_stream), "group"))) return rc;
-  if ((rc = launched(launch_tiles(off, L->ne, tiles, ntiles, g_stream), "tiles"))) return rc;
-  if ((rc = launched(launch_to_f16(h2, x16, (uint64_t)T * L->dm, g_stream), "to f16"))) return rc;
+  if ((rc = launched(launch_group(ids, n, L->nk, L->ne, off, xmap, inv, h2, x16, (uint64_t)T * L->dm, g_stream),
+                     "group + f16 activations")))
+    return rc;
   stage_end(ST_Q8X);
   const uint64_t rbg = row_bytes(fg, L->dm), rbd = row_bytes(fd, L->ef);
   const uint32_t maxt = n / gemm_bm() + L->ne + 1;  // >= sum over experts of ceil(M_e / BM)
@@ -375,8 +371,7 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
   g.arows = T;
   g.xmap = xmap;
   g.off = off;
-  g.tiles = tiles;
-  g.ntiles = ntiles;
+  g.ne = L->ne;
   g.out = gb + gs.act;
   if (L->PG && L->PU) {
     g.P0 = dp<uint8_t>(L->PG);
@@ -714,7 +709,7 @@ int llb_moe_hip_group(llb_dptr ids, uint32_t n, uint32_t nk, uint32_t ne, llb_dp
   if (!ne || !nk || n % nk) return fail(LLB_HIP_EINVAL, "group: n must be a multiple of nk");
   if (scratch_bytes < (size_t)(ne + 1) * 4) return fail(LLB_HIP_ESCRATCH, "group: scratch < (ne + 1) * 4 bytes");
   return launched(launch_group(dp<uint32_t>(ids), n, nk, ne, dp<uint32_t>(off), dp<uint32_t>(xmap), dp<uint32_t>(inv),
-                               dp<uint32_t>(scratch), g_stream),
+                               nullptr, nullptr, 0, g_stream),
                   "group");
 }
 

@@ -1118,12 +1118,16 @@ int launch_tree_rows(const TreeArgs& a, u32 nsp, hipStream_t st) {
   for (u32 i = 0; i < a.nseg; i++) rows += a.seg[i].rows;
   if (rows == 0) return 0;
   if (a.T >= 16 && nsp <= 2) {  // token tiles: weights read once a tile
-    const u32 tt = 4, rw = nsp == 1 ? 4u : 2u;
+    const u32 tt = 4, nt = (a.T + tt - 1) / tt, slots = 2 * cu_count();
     const size_t sm = (size_t)tt * 64 * (32 * nsp + 4) * 4;
+    // rows a wave: 4 (2 for two-span rows), which reads a token's x from LDS once per 4 rows, unless
+    // the grid would then not fill one round of resident blocks (few tokens: batched decode); then 1
+    u32 rw = nsp == 1 ? 4u : 2u;
+    if ((u64)((rows + 4 * rw - 1) / (4 * rw)) * nt < slots) rw = 1;
     // tiles a block: the count that minimises (rounds of resident blocks) x (tiles a block + 2, a
     // block's own cost of loading its rows and filling its pipeline), two blocks resident a CU -- a
     // grid just past one round of blocks would otherwise take two
-    const u32 rb = (rows + 4 * rw - 1) / (4 * rw), nt = (a.T + tt - 1) / tt, slots = 2 * cu_count();
+    const u32 rb = (rows + 4 * rw - 1) / (4 * rw);
     u32 ntb = 1;
     u64 best = ~0ull;
     for (u32 n = 1; n <= nt; n++) {
@@ -1131,14 +1135,18 @@ int launch_tree_rows(const TreeArgs& a, u32 nsp, hipStream_t st) {
       if (cost < best) { best = cost; ntb = n; }
     }
     const dim3 grid(rb, (nt + ntb - 1) / ntb);
-    static bool set1 = false, set2 = false;
-    if (nsp == 1) {
-      if (!set1) { (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<1, 4, 4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm); set1 = true; }
-      LAUNCH_K((k_tree_rows_mt<1, 4, 4>), grid, dim3(256), sm, st, a, ntb);
-    } else {
-      if (!set2) { (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<2, 4, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm); set2 = true; }
-      LAUNCH_K((k_tree_rows_mt<2, 4, 2>), grid, dim3(256), sm, st, a, ntb);
+    static bool set = false;
+    if (!set) {
+      (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<1, 4, 4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(4 * 64 * 36 * 4));
+      (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<1, 4, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(4 * 64 * 36 * 4));
+      (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<2, 4, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(4 * 64 * 68 * 4));
+      (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<2, 4, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(4 * 64 * 68 * 4));
+      set = true;
     }
+    if (nsp == 1 && rw == 4) LAUNCH_K((k_tree_rows_mt<1, 4, 4>), grid, dim3(256), sm, st, a, ntb);
+    else if (nsp == 1) LAUNCH_K((k_tree_rows_mt<1, 4, 1>), grid, dim3(256), sm, st, a, ntb);
+    else if (rw == 2) LAUNCH_K((k_tree_rows_mt<2, 4, 2>), grid, dim3(256), sm, st, a, ntb);
+    else LAUNCH_K((k_tree_rows_mt<2, 4, 1>), grid, dim3(256), sm, st, a, ntb);
     return 0;
   }
   const u32 rpw = tree_rows_per_wave(nsp);

@@ -22,41 +22,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 #define G3_BM GM_BM
 
 
-// f32 rows -> f16 rows (the activations' one conversion)
-__global__ void __launch_bounds__(256) k_to_f16(const float* __restrict__ x, _Float16* __restrict__ y, u64 n) {
-  const u64 i = ((u64)blockIdx.x * 256 + threadIdx.x) * 4;
-  if (i + 3 < n) {
-    const float4 v = *(const float4*)(x + i);
-    y[i] = (_Float16)v.x; y[i + 1] = (_Float16)v.y; y[i + 2] = (_Float16)v.z; y[i + 3] = (_Float16)v.w;
-  } else {
-    for (u64 k = i; k < n; k++) y[k] = (_Float16)x[k];
-  }
-}
-
-// the tile list: for each expert, ceil(M_e / BM) tiles (e << 16 | tile index); count in *ntiles
-__global__ void __launch_bounds__(1024) k_tiles(const u32* __restrict__ off, u32 ne, u32* __restrict__ tiles,
-                                                u32* __restrict__ ntiles) {
-  __shared__ u32 part[1024];
-  const u32 t = threadIdx.x;
-  // experts t, t + 1024, ... (ne may exceed 1024): each thread counts its experts' tiles
-  u32 mine = 0;
-  for (u32 e = t; e < ne; e += 1024) mine += (off[e + 1] - off[e] + GM_BM - 1) / GM_BM;
-  part[t] = mine;
-  __syncthreads();
-  for (u32 s = 1; s < 1024; s <<= 1) {  // inclusive scan
-    const u32 v = t >= s ? part[t - s] : 0u;
-    __syncthreads();
-    part[t] += v;
-    __syncthreads();
-  }
-  u32 at = part[t] - mine;
-  for (u32 e = t; e < ne; e += 1024) {
-    const u32 nt = (off[e + 1] - off[e] + GM_BM - 1) / GM_BM;
-    for (u32 k = 0; k < nt; k++) tiles[at++] = e << 16 | k;
-  }
-  if (t == 1023) *ntiles = part[1023];
-}
-
 // ---- packed weights: a matrix of R rows x K columns re-laid in tiles of 32 rows x 64 columns, tile
 // (g, t) = rows 32 g .. 32 g + 31, columns 64 t .. 64 t + 63 at byte (g K / 64 + t) PK_TB<F>. In a
 // tile, lane l = 32 h + r owns row r, columns 32 h .. 32 h + 31: exactly the GEMM's B operand for a
@@ -401,18 +366,75 @@ DEV void gemm3_body(const GemmArgs& g, _Float16* lds, u32 e, u32 base, u32 m0, u
 // 8 NT ceil(max tiles / 8) blocks). Blocks a CU: three on packed weights, two on GGUF rows (whose
 // wider per-lane loads need more registers) and for packed Q8_0 gate / up (which would spill at three).
 constexpr int g3_blocks(u32 F, u32 MODE, bool PKD) { return PKD && !(F == FM_Q8_0 && MODE == 0) ? 3 : 2; }
+// The tile list, read off the slot offsets: expert e has ceil(M_e / BM) slot tiles, listed in expert
+// order. Every wave loads the ne + 1 offsets once (16 chunks of 64 experts at most, all loads in
+// flight together), sums the tile counts, and finds tile `tile` by an inclusive scan of the counts
+// and a ballot -- no list to build, so no launch between the dispatch and the GEMM.
+#define G3_NEC 16  // chunks of 64 experts: ne <= 1024
+DEV u32 wave_scan_incl(u32 v, u32 L) {
+#pragma unroll
+  for (u32 m = 1; m < 64; m <<= 1) {
+    const u32 o = __shfl_up(v, m, 64);
+    if (L >= m) v += o;
+  }
+  return v;
+}
+DEV void tiles_load(const u32* __restrict__ off, u32 ne, u32 L, u32* te) {
+#pragma unroll
+  for (u32 c = 0; c < G3_NEC; c++) {
+    const u32 e = 64 * c + L;
+    te[c] = e < ne ? (off[e + 1] - off[e] + G3_BM - 1) / G3_BM : 0u;
+  }
+}
+DEV u32 tiles_total(const u32* te, u32 ne) {
+  u32 s = 0;
+#pragma unroll
+  for (u32 c = 0; c < G3_NEC; c++) s += 64 * c < ne ? te[c] : 0u;
+#pragma unroll
+  for (u32 m = 1; m < 64; m <<= 1) s += __shfl_xor(s, m, 64);
+  return s;
+}
+// tile < the total: its expert and its slot tile within the expert
+DEV void tiles_find(const u32* te, u32 ne, u32 tile, u32 L, u32& e, u32& k) {
+  u32 acc = 0;
+  e = 0;
+  k = 0;
+#pragma unroll
+  for (u32 c = 0; c < G3_NEC; c++) {
+    if (64 * c >= ne) break;
+    const u32 inc = wave_scan_incl(te[c], L), tot = __shfl(inc, 63, 64);
+    if (tile < acc + tot) {  // uniform: tile, acc and tot are the same on every lane
+      const u64 b = __ballot(acc + inc > tile);
+      const u32 f = (u32)__builtin_ctzll(b);
+      e = 64 * c + f;
+      k = tile - acc - __shfl(inc - te[c], (int)f, 64);
+      break;
+    }
+    acc += tot;
+  }
+}
+
 template <u32 F, u32 MODE, bool PKD>
 __global__ void __launch_bounds__(256, g3_blocks(F, MODE, PKD)) k_moe_gemm3(GemmArgs g, u32 NT) {
   extern __shared__ _Float16 lds[];
-  const u32 q = blockIdx.x >> 3, ntile = q % NT;
-  const u32 ntl = g.tiles ? *g.ntiles : (g.M + G3_BM - 1) / G3_BM, C = (ntl + 7) / 8;
+  const u32 q = blockIdx.x >> 3, ntile = q % NT, L = threadIdx.x & 63;
+  u32 te[G3_NEC];
+  u32 ntl;
+  if (g.off) {
+    tiles_load(g.off, g.ne, L, te);
+    ntl = __builtin_amdgcn_readfirstlane(tiles_total(te, g.ne));
+  } else {
+    ntl = (g.M + G3_BM - 1) / G3_BM;
+  }
+  const u32 C = (ntl + 7) / 8;
   const u32 tile = (blockIdx.x & 7) * C + q / NT;
   if (q / NT >= C || tile >= ntl) return;
   u32 e, m0, base, M;
-  if (g.tiles) {
-    const u32 tv = g.tiles[tile];
-    e = tv >> 16;
-    m0 = (tv & 0xffffu) * G3_BM;
+  if (g.off) {
+    u32 k;
+    tiles_find(te, g.ne, tile, L, e, k);
+    e = __builtin_amdgcn_readfirstlane(e);
+    m0 = __builtin_amdgcn_readfirstlane(k) * G3_BM;
     base = g.off[e];
     M = g.off[e + 1] - base;
   } else {
@@ -487,6 +509,7 @@ int launch_moe_gemm(const GemmArgs& g, u32 fm, u32 mode, u32 grid_y, hipStream_t
   const u32 nf = mode == 0 ? 128u : 256u;
   // A's buffer loads take 32-bit offsets below 2^31 (dead rows use 2^31)
   if (g.K % G3_BK || g.N % nf || fm == FM_F32 || (u64)g.arows * g.K * 2 >= (1ull << 31)) return -1;
+  if (g.off && (g.ne == 0 || g.ne > 64 * G3_NEC)) return -1;
   const dim3 grid(8 * (g.N / nf) * ((grid_y + 7) / 8));
   const size_t sm = (size_t)2 * G3_STAGE * 2;
   const bool pk = g.P0 != nullptr;
@@ -521,14 +544,6 @@ int launch_pack(u32 fm, const u8* W, u64 es, u64 rb, u32 R, u32 K, u32 ne, u8* P
   return -1;
 }
 
-int launch_to_f16(const float* x, _Float16* y, u64 n, hipStream_t st) {
-  hipLaunchKernelGGL(k_to_f16, dim3((u32)((n / 4 + 255) / 256 + 1)), dim3(256), 0, st, x, y, n);
-  return 0;
-}
-int launch_tiles(const u32* off, u32 ne, u32* tiles, u32* ntiles, hipStream_t st) {
-  hipLaunchKernelGGL(k_tiles, dim3(1), dim3(1024), 0, st, off, ne, tiles, ntiles);
-  return 0;
-}
 int launch_combine(const float* out, const u32* inv, const float* wt, u32 nk, const float* shd, const float* sgo,
                    const float* x1, float* y, u32 dm, u32 T, hipStream_t st) {
   if (dm % 4 || nk > 64) return -1;

@@ -40,13 +40,35 @@ int launch_q8_1(const float* x, uint32_t n, int8_t* q, float2* ds, hipStream_t s
 // Block e; thread t scans the contiguous slots [t per, t per + per): ids below e (the expert's offset)
 // and equal to e (its hits); an exclusive scan of the hits over the block gives each thread its first
 // position, and it writes its hits in slot order -- the stable order, with one scan a block.
+// Blocks past ne (when x16 is set) convert the activations to f16 for the grouped GEMM instead, 8
+// values a thread (nx % 8 == 0): the two jobs are independent and share one launch.
 __global__ void __launch_bounds__(256) k_group(const u32* __restrict__ ids, u32 n, u32 nk, u32 ne, u32* __restrict__ off,
-                                               u32* __restrict__ xmap, u32* __restrict__ inv) {
+                                               u32* __restrict__ xmap, u32* __restrict__ inv,
+                                               const float* __restrict__ x, _Float16* __restrict__ x16, u64 nx) {
   __shared__ u32 wl[4], wh[4];
+  if (blockIdx.x >= ne) {
+    const u64 i = ((u64)(blockIdx.x - ne) * 256 + threadIdx.x) * 8;
+    if (i < nx) {
+      const float4 a = *(const float4*)(x + i), b = *(const float4*)(x + i + 4);
+      typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+      const h8 v = {(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+                    (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
+      *(h8*)(x16 + i) = v;
+    }
+    return;
+  }
   const u32 e = blockIdx.x, t = threadIdx.x, w = t >> 6, L = t & 63;
   const u32 per = (n + 255) / 256, i0 = min(t * per, n), i1 = min(i0 + per, n);
-  u32 lt = 0, hit = 0;
-  for (u32 i = i0; i < i1; i++) {
+  u32 lt = 0, hit = 0, i = i0;
+  if (per % 4 == 0 && ((uintptr_t)ids & 15) == 0) {  // whole uint4s from i0 (i0 = t per), loads in flight together
+#pragma unroll 4
+    for (; i + 4 <= i1; i += 4) {
+      const uint4 v = *(const uint4*)(ids + i);
+      lt += (v.x < e ? 1u : 0u) + (v.y < e ? 1u : 0u) + (v.z < e ? 1u : 0u) + (v.w < e ? 1u : 0u);
+      hit += (v.x == e ? 1u : 0u) + (v.y == e ? 1u : 0u) + (v.z == e ? 1u : 0u) + (v.w == e ? 1u : 0u);
+    }
+  }
+  for (; i < i1; i++) {
     const u32 v = ids[i];
     lt += v < e ? 1u : 0u;
     hit += v == e ? 1u : 0u;
@@ -81,9 +103,11 @@ __global__ void __launch_bounds__(256) k_group(const u32* __restrict__ ids, u32 
 }
 
 int launch_group(const uint32_t* ids, uint32_t n, uint32_t nk, uint32_t ne, uint32_t* off, uint32_t* xmap,
-                 uint32_t* inv, uint32_t* cnt, hipStream_t st) {
-  (void)cnt;
-  hipLaunchKernelGGL(k_group, dim3(ne), dim3(256), 0, st, ids, n, nk, ne, off, xmap, inv);
+                 uint32_t* inv, const float* x, _Float16* x16, uint64_t nx, hipStream_t st) {
+  if (x16 && nx % 8) return -1;
+  const u64 nconv = x16 ? (nx + 2047) / 2048 : 0;
+  if (ne + nconv > 0x7fffffffull) return -1;
+  hipLaunchKernelGGL(k_group, dim3((u32)(ne + nconv)), dim3(256), 0, st, ids, n, nk, ne, off, xmap, inv, x, x16, nx);
   return 0;
 }
 

@@ -1,6 +1,6 @@
 """The grouped GEMM's index arithmetic (k_moe_gemm3 and launch_moe_gemm in
 eureka-engine_amd/csrc/moe_gemm.hip), restated on the host and run over every block, thread and k-tile
-of real tile lists: every global read stays inside its buffer (activation rows past a tile's slots
+of real tile lists (read off the slot offsets by a wave scan, restated below): every global read stays inside its buffer (activation rows past a tile's slots
 carry an offset past A's buffer bound, which the buffer load answers with zeros and no access), every
 weight read inside its expert's rows and columns, every LDS access inside its stage, every store inside
 the output, and every (slot, output column) written exactly once. Shapes: the 2048-token prefill,
@@ -178,3 +178,51 @@ def test_pack_and_packed_reads(fm, R, K, ne):
                         base = (ne - 1) * tiles * TB + (g * nkt + t) * TB
                         for off, n in PK_READS[fm]:
                             assert (base + off(l) + n).max() <= total
+
+
+# the tile list read off the slot offsets (tiles_load / tiles_total / tiles_find in k_moe_gemm3): lane L of a
+# wave holds the tile counts of experts 64 c + L, c < 16; the total is a wave sum; tile i is found by an
+# inclusive scan of each chunk and the first lane whose running count passes i
+NEC = 16
+
+
+def tiles_emulated(off, ne):
+    assert ne <= 64 * NEC and len(off) == ne + 1
+    L = np.arange(64)
+    te = np.zeros((NEC, 64), np.int64)
+    for c in range(NEC):
+        e = 64 * c + L
+        ok = e < ne
+        te[c, ok] = (off[e[ok] + 1] - off[e[ok]] + BM - 1) // BM
+    total = int(sum(te[c].sum() for c in range(NEC) if 64 * c < ne))
+
+    def find(tile):
+        acc = 0
+        for c in range(NEC):
+            if 64 * c >= ne:
+                break
+            inc = np.cumsum(te[c])
+            tot = int(inc[63])
+            if tile < acc + tot:
+                f = int(np.flatnonzero(acc + inc > tile)[0])
+                return 64 * c + f, tile - acc - int(inc[f] - te[c, f])
+            acc += tot
+        raise AssertionError("tile past the total")
+    return total, find
+
+
+@pytest.mark.parametrize("ne,n,seed,skew", [(128, 512, 0, 1.1), (128, 16384, 1, None), (512, 5130, 2, 1.1),
+                                           (1024, 8192, 3, 1.1), (1, 300, 4, None), (65, 64, 5, None),
+                                           (1000, 10, 6, None), (200, 0, 7, None)])
+def test_tiles_from_offsets(ne, n, seed, skew):
+    rng = np.random.default_rng(seed)
+    p = np.ones(ne) if skew is None else 1.0 / np.arange(1, ne + 1) ** skew
+    ids = rng.choice(ne, n, p=p / p.sum()) if n else np.zeros(0, np.int64)
+    cnt = np.bincount(ids, minlength=ne)
+    off = np.concatenate([[0], np.cumsum(cnt)])
+    tl = [(e, k) for e in range(ne) for k in range((cnt[e] + BM - 1) // BM)]
+    total, find = tiles_emulated(off, ne)
+    assert total == len(tl) and total <= n // BM + ne + 1   # the grid's bound
+    for i, (e, k) in enumerate(tl):
+        assert find(i) == (e, k)
+        assert 0 <= k * BM < cnt[e]                         # a live slot tile: m0 < M

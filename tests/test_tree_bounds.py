@@ -14,7 +14,10 @@ def launch(nsp, T, rows, cus=256):
     """launch_tree_rows' choice for T >= 16, nsp <= 2: TT, dynamic LDS bytes, ntb, grid, rows a wave"""
     tt, rw = 4, (4 if nsp == 1 else 2)
     sm = tt * 64 * (32 * nsp + 4) * 4
-    rb, nt, slots = (rows + 4 * rw - 1) // (4 * rw), (T + tt - 1) // tt, 2 * cus
+    nt, slots = (T + tt - 1) // tt, 2 * cus
+    if (rows + 4 * rw - 1) // (4 * rw) * nt < slots:   # short of one round of resident blocks: a row a wave
+        rw = 1
+    rb = (rows + 4 * rw - 1) // (4 * rw)
     ntb, best = 1, None
     for n in range(1, nt + 1):
         cost = (rb * ((nt + n - 1) // n) + slots - 1) // slots * (n + 2)
@@ -89,7 +92,7 @@ def check(nsp, cols, T, segrows, wfmt_bytes=4):
 @pytest.mark.parametrize("nsp,cols,T,segrows", [
     (1, 2048, 2048, [128]),             # prefill router, 2048 tokens
     (1, 2048, 513, [512, 1]),           # config 5: 512 experts + the shared gate row
-    (1, 2048, 64, [128]),               # 64-token batches
+    (1, 2048, 64, [128]),               # 64-token batches (a row a wave)
     (1, 2048, 64, [256, 1]),
     (1, 1536, 33, [1000]),              # ragged: 33 tokens, 1000 rows, 1536 columns (dead lanes)
     (1, 2048, 16, [7, 1]),              # fewest tokens on this path, rows not a multiple of 8
@@ -107,3 +110,8 @@ def test_tree_mt_grid_covers_tokens():
                 TT, _, ntb, (gx, gy), RW = launch(nsp, T, rows, cus=(256, 80, 304)[(T + rows) % 3])
                 assert gx * 4 * RW >= rows
                 assert gy * ntb * TT >= T and (gy - 1) * ntb * TT < T
+
+
+def test_tree_mt_rows_a_wave():
+    assert launch(1, 64, 128)[4] == 1 and launch(1, 2048, 128)[4] == 4 and launch(1, 513, 513)[4] == 4
+    assert launch(2, 20, 41)[4] == 1 and launch(2, 1000, 65)[4] == 2
