@@ -336,7 +336,9 @@ def test_f16_tier_config5_mixed(dev):
     assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
 
 
-PACK_CASES = [(f"small{i}", i, 150) for i in range(len(SMALL))] + [("c1", None, 300), ("c1k", None, 300), ("c2", None, 40)]
+# includes a 2048-token chunk and config 5's 1025 tokens over 512 experts (ragged tiles, shared expert)
+PACK_CASES = [(f"small{i}", i, 150) for i in range(len(SMALL))] + [("c1", None, 300), ("c1k", None, 300), ("c2", None, 40),
+                                                                   ("c1", None, 2048), ("c5", None, 1025)]
 
 
 @pytest.mark.parametrize("name,si,T", PACK_CASES)
