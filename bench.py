@@ -277,27 +277,68 @@ def residency_leg(dev, shape, tokens=16):
     return out
 
 
-def cpu_baseline(shape, seconds=12.0):
-    """the CPU oracle's exact layer, single thread, on tokens of layer 0 (experts generated first)."""
+def hbm_copy_leg(dev, nbytes=1 << 30, reps=20):
+    """achievable HBM bandwidth: device-to-device copies of 1 GiB (read + write bytes over wall time, one sync
+    around the batch), beside the 8 TB/s datasheet peak the roofline fractions use"""
+    src, dst = dev.alloc(nbytes), dev.alloc(nbytes)
+    dev.check(dev.lib.llb_hip_copy(dst, src, nbytes))
+    dev.sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        dev.check(dev.lib.llb_hip_copy(dst, src, nbytes))
+    dev.sync()
+    dt = time.perf_counter() - t0
+    dev.free(src)
+    dev.free(dst)
+    gbs = 2 * nbytes * reps / dt / 1e9
+    return {"gbs": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "config": f"{reps} device-to-device copies of {nbytes >> 20} MiB (hipMemcpyAsync), read + write bytes"}
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(shape, seconds=12.0, threads=1):
+    """the CPU oracle's exact layer on tokens of layer 0 (experts generated first, outside the timer): one
+    thread, and with threads > 1 also the rows-parallel OpenMP variant on the same tokens. Returns
+    (single, threaded or None)."""
     import oracle_lib as ol
     hl = ol.HostLayer(shape, seed=0, layer=0, experts=[])
-    n, spent, t = 0, 0.0, 0
+    n, spent, spent_mt, t = 0, 0.0, 0.0, 0
     while spent < seconds and n < 64:
         h2 = ol.gauss(0, ol.ST_H2, t * shape.dm, shape.dm).reshape(1, shape.dm)
         ids, _, _ = hl.route(h2)
         hl.add_experts(np.unique(ids))
         hl._mk()
-        y = np.zeros((1, shape.dm), np.float32)
-        i2, w2, s2 = np.zeros((1, shape.nk), np.uint32), np.zeros((1, shape.nk), np.float32), np.zeros(1, np.float32)
-        t0 = time.perf_counter()
-        rc = ol.lib().mo_moe_exact(C.byref(hl.desc), 1, ol.ptr(h2), None, ol.ptr(y), ol.ptr(i2), ol.ptr(w2), ol.ptr(s2), 1)
-        spent += time.perf_counter() - t0
-        assert rc == 0
+        for nt in ((1, threads) if threads > 1 else (1,)):
+            y = np.zeros((1, shape.dm), np.float32)
+            i2, w2, s2 = np.zeros((1, shape.nk), np.uint32), np.zeros((1, shape.nk), np.float32), np.zeros(1, np.float32)
+            t0 = time.perf_counter()
+            rc = ol.lib().mo_moe_exact(C.byref(hl.desc), 1, ol.ptr(h2), None, ol.ptr(y), ol.ptr(i2), ol.ptr(w2),
+                                       ol.ptr(s2), nt)
+            dt = time.perf_counter() - t0
+            assert rc == 0
+            if nt == 1:
+                spent += dt
+            else:
+                spent_mt += dt
         n += 1
         t += 1
-    return {"value": spent / n * 1e6, "unit": "us/token-layer", "cores": 1, "kind": "port",
-            "sample": f"{n} decode tokens of one {shape.ne}-expert layer through the oracle's exact tier "
-                      f"(oracle/moe_oracle.c, -O2 -ffp-contract=off, 1 thread); expert generation outside the timer"}
+
+    def rec(sec, nt):
+        return {"value": sec / n * 1e6, "unit": "us/token-layer", "cores": nt, "kind": "port",
+                "sample": f"{n} decode tokens of one {shape.ne}-expert layer through the oracle's exact tier "
+                          f"(oracle/moe_oracle.c, -O2 -ffp-contract=off, {nt} thread{'s' if nt > 1 else ''}"
+                          f"{', OpenMP over rows' if nt > 1 else ''}); expert generation outside the timer; "
+                          f"host CPU {cpu_model()}, {os.cpu_count()} logical CPUs visible"}
+    return rec(spent, 1), (rec(spent_mt, threads) if threads > 1 else None)
 
 
 def main():
@@ -315,9 +356,10 @@ def main():
     ap.add_argument("--prefill-T", type=int, default=2048)
     ap.add_argument("--no-c5", dest="c5", action="store_false",
                     help="skip the config-5 leg (48 resident 512-expert layers, 1 + 512 tokens a launch)")
-    ap.add_argument("--legs", default="q8,batched,prefill,prefill_k,c5,rmsnorm,residency",
+    ap.add_argument("--legs", default="q8,batched,prefill,prefill_k,c5,rmsnorm,residency,copy",
                     help="legs after the decode line: q8 (the int8 tier's decode), batched (config 3), prefill (c1), "
-                         "prefill_k (c1k), c5, rmsnorm, residency (GGUF stacks in each residency mode)")
+                         "prefill_k (c1k), c5, rmsnorm, residency (GGUF stacks in each residency mode), copy "
+                         "(achievable HBM bandwidth)")
     ap.add_argument("--traffic-from", metavar="DIR",
                     help="only write profiles/traffic.json from the PMC csv directories under DIR and exit")
     ap.add_argument("--copy-calib", action="store_true",
@@ -476,8 +518,14 @@ def main():
         out["residency_gguf"] = residency_leg(dev, shape)
     if "rmsnorm" in legs:
         out["rmsnorm_add"] = rmsnorm_leg(dev, shape.dm)
+    if "copy" in legs:
+        out["hbm_copy"] = hbm_copy_leg(dev)
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(shape)
+        # and the rows-parallel variant on the box's CPU share (OMP_NUM_THREADS, 16 on the GPU boxes)
+        nt = max(1, min(int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1), 64))
+        out["cpu_baseline"], mt = cpu_baseline(shape, threads=nt)
+        if mt:
+            out["cpu_baseline_threads"] = mt
     print(json.dumps(out), flush=True)
 
 
