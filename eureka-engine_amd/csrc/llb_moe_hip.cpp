@@ -13,7 +13,7 @@ int launch_gauss(uint64_t seed, uint64_t stream, uint64_t i0, uint64_t n, float 
 int launch_gen_rows(uint32_t fm, uint64_t seed, uint64_t stream, uint64_t r0, uint64_t nr, uint32_t cols, float sigma,
                     uint8_t* out, hipStream_t st);
 int moe_q8_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const float* x1, float* y, const uint32_t* ids,
-                   const float* wt, const float* sgo, uint8_t* scratch, hipStream_t st);
+                   const float* wt, const float* sgo, const TopkArgs* tk, uint8_t* sc, hipStream_t st);
 size_t moe_q8_scratch(const llb_moe_layer* L, uint32_t T);
 int launch_group(const uint32_t* ids, uint32_t n, uint32_t nk, uint32_t ne, uint32_t* off, uint32_t* xmap,
                  uint32_t* inv, const float* x, _Float16* x16, uint64_t nx, hipStream_t st);
@@ -538,8 +538,10 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
   if (streamed && (tier != LLB_MOE_EXACT || T != 1 || g_capturing))
     return fail(LLB_HIP_EINVAL, "stream residency: the exact tier, one token, outside graph capture");
   TopkArgs tk{};
-  const bool fuse_topk = tier == LLB_MOE_EXACT && fg == fu && T == 1 && !streamed;
-  if ((rc = route(L, T, dp<float>(h2), dp<uint32_t>(ids), dp<float>(wt), sc, s, true, fuse_topk ? &tk : nullptr)))
+  const bool fuse_topk = (tier == LLB_MOE_Q8 || fg == fu) && T == 1 && !streamed;
+  // the q8 tier computes the shared gate / up rows in its own gate / up launch (int8 dots)
+  if ((rc = route(L, T, dp<float>(h2), dp<uint32_t>(ids), dp<float>(wt), sc, s, tier != LLB_MOE_Q8,
+                  fuse_topk ? &tk : nullptr)))
     return rc;
   const uint64_t rbg = row_bytes(fg, L->dm), rbu = row_bytes(fu, L->dm);
   const uint64_t esg = (uint64_t)(fz ? 2 : 1) * L->ef * rbg;
@@ -547,7 +549,7 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
   const uint8_t* U = fz ? G + (uint64_t)L->ef * rbg : dp<uint8_t>(L->U);
   if (tier == LLB_MOE_Q8) {
     rc = moe_q8_forward(L, T, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt),
-                        (const float*)(sc + s.sgo), sc + s.total, g_stream);
+                        (const float*)(sc + s.sgo), fuse_topk ? &tk : nullptr, sc + s.total, g_stream);
     return launched(rc, "q8 tier");
   }
   GuArgs g{};

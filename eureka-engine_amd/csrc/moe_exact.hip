@@ -17,6 +17,7 @@
 //           (lane ^ 2, lane ^ 1), levels 4, 2, 1 stay in registers.
 #include "moe_dev.h"
 #include "moe_kernels.h"
+#include "moe_q8dot.h"
 
 // phase timestamps for latency studies: a build that defines MOE_PHASE_T gets (block 0, thread 0)
 // wall-clock stamps (100 MHz) in moe_phase_t[]; the library build compiles them away
@@ -816,6 +817,74 @@ __global__ void __launch_bounds__(256) k_gu_topk(GuArgs a, TopkArgs k) {
   if ((tid & 15) == 0) a.act[(u64)slot * a.ef + r] = silu_mul(s, u);
   PHASE(12);
   BSTAMP(2, 1);
+}
+
+// the q8 tier's gate + up + SwiGLU (llb_mx_gu): 256 threads = 32 row pairs of one slot, 4 lanes a row
+// (row_q8), gate rows on lane groups 0..7 of a half wave and up rows on 8..15, so lane 32 + L holds
+// the up dot of lane L's gate row. Tasks past the T nk ef routed rows are the shared expert's gate /
+// up rows of token (task - T nk ef) / sf. With lq the block quantizes its token's x to q8_1 in LDS
+// (k_q8_1's steps, the same bits); with top-k (one token) a routed block also recomputes the token's
+// routing first (topk_body256, as k_gu_topk) and the token's first block writes ids / wt / sgo.
+__global__ void __launch_bounds__(256) k_gu_q8(Q8Args a, TopkArgs k, u32 nslot, u32 lq, u32 topk) {
+  extern __shared__ float4 gsm4[];  // [TOPK_LDS] routing (with top-k), then xq [dm], xd [dm / 32]
+  float* sm = (float*)gsm4;
+  const u32 tid = threadIdx.x, L = tid & 63, q = L >> 2, p = L & 3;
+  const u32 pr = 8 * (tid >> 6) + (q & 7);
+  const u32 task0 = blockIdx.x * 32;
+  const bool routed = task0 < nslot * a.ef;
+  u32 slot = 0, row, t;
+  if (routed) {
+    slot = task0 / a.ef;
+    row = task0 % a.ef + pr;
+    t = slot / a.nk;
+  } else {
+    const u32 kk = task0 - nslot * a.ef;
+    t = kk / a.sf;
+    row = kk % a.sf + pr;
+  }
+  // x in LDS or in memory: two call sites below, so each pointer keeps its address space (a select
+  // between the two would make flat loads, whose waits also wait for the weight loads)
+  signed char* lxq = (signed char*)(sm + (topk ? TOPK_LDS : 0));
+  float2* lxd = (float2*)(lxq + a.dm);
+  if (lq) q8_1_block256<16>(a.h2 + (u64)t * a.dm, a.dm, lxq, lxd);
+  u64 e = 0;
+  if (routed) {
+    if (topk) {  // block-uniform
+      topk_body256(k, t, sm, false);
+      e = ((const u32*)(sm + TOPK_SIDS))[slot % a.nk];
+      if (task0 % a.ef == 0 && slot % a.nk == 0) topk_write(k, t, sm);
+    } else {
+      e = a.ids[slot];
+    }
+  }
+  if (lq) __syncthreads();  // x in LDS (topk_body256 ends on a barrier too)
+  const u8* w;
+  u32 f;
+  float* out;
+  if (routed) {
+    w = q < 8 ? a.G + e * a.es + row * a.rbg : a.U + e * a.es + row * a.rbu;
+    f = q < 8 ? a.fg : a.fu;
+    out = a.act + (u64)slot * a.ef + row;
+  } else {
+    w = q < 8 ? a.SG + (u64)row * a.rbsg : a.SU + (u64)row * a.rbsu;
+    f = q < 8 ? a.fsg : a.fsu;
+    out = a.sa + (u64)t * a.sf + row;
+  }
+  const float v = lq ? row_q8_fm<8>(f, w, a.dm, lxq, lxd, p)
+                     : row_q8_fm<8>(f, w, a.dm, a.hq + (u64)t * a.dm, a.hd + (u64)t * (a.dm / 32), p);
+  const float u = __shfl_xor(v, 32, 64);
+  if (q < 8 && p == 0) *out = silu_mul(v, u);
+}
+
+int launch_gu_q8(const Q8Args& a, const TopkArgs* tk, u32 nslot, u32 T, bool lq, hipStream_t st) {
+  if (a.ef % 32 || a.sf % 32 || a.dm % 32 || (tk && (T != 1 || tk->ne > 1024 || tk->nk > 64))) return -1;
+  if (lq && a.dm > 16 * 256) return -1;
+  const u32 tasks = (u32)(((u64)nslot * a.ef + (u64)T * a.sf) / 32);
+  const size_t sm = (tk ? (size_t)TOPK_LDS * 4 : 0) + (lq ? (size_t)a.dm * 5 / 4 : 0);
+  if (sm > 65536) return -1;
+  const TopkArgs k = tk ? *tk : TopkArgs{};
+  LAUNCH_K(k_gu_q8, dim3(tasks), dim3(256), sm, st, a, k, nslot, (u32)lq, (u32)(tk != nullptr));
+  return 0;
 }
 
 // down + rank-order combine + gated shared expert + residual, 8 lanes a row. A block takes R

@@ -92,6 +92,7 @@ struct Q8Args {
   uint64_t rbg, rbu, rbd, es, rbsg, rbsu, rbs;
   uint32_t fg, fu, fd, fsg, fsu, fsd;
   uint32_t dm, ef, nk, sf, rw;
+  const float* h2;   // [T][dm] activations (quantized in LDS by the gate / up kernel for few tokens)
   const int8_t* hq;  // [T][dm] q8_1 of h2
   const float2* hd;  // [T][dm / 32]
   const uint32_t* ids;
@@ -106,6 +107,9 @@ struct Q8Args {
   const float* x1;
   float* y;
 };
+// the q8 tier's gate / up + SwiGLU (shared expert rows ride along); tk: route inside the launch (T = 1);
+// lq: quantize the token's activations in LDS instead of reading hq / hd
+int launch_gu_q8(const Q8Args& a, const TopkArgs* tk, uint32_t nslot, uint32_t T, bool lq, hipStream_t st);
 struct GemmArgs {
   const uint8_t* W0;  // weights (gate / the one matrix), rows of K columns
   const uint8_t* W1;  // up (mode 0)

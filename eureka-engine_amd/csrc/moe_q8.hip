@@ -6,6 +6,7 @@
 #include "../../include/llb_moe_hip.h"
 #include "moe_dev.h"
 #include "moe_kernels.h"
+#include "moe_q8dot.h"
 
 // ---------------------------------------------------------------- q8_1 (pf_q8x)
 
@@ -14,16 +15,10 @@
 __global__ void __launch_bounds__(256) k_q8_1(const float* __restrict__ x, u32 n, signed char* __restrict__ q,
                                               float2* __restrict__ ds) {
   const u64 i = (u64)blockIdx.x * 256 + threadIdx.x;
-  const float v = i < n ? x[i] : 0.0f;
-  float a = fabsf(v), s = v;
-#pragma unroll
-  for (u32 m = 16; m > 0; m >>= 1) {
-    a = fmaxf(a, __shfl_xor(a, m, 64));
-    s = s + __shfl_xor(s, m, 64);
-  }
-  const float d = a / 127.0f;
-  if (i < n) q[i] = a == 0.0f ? (signed char)0 : (signed char)max(-127, min(127, (int)roundf(v / d)));
-  if (i < n && (threadIdx.x & 31) == 0) ds[i >> 5] = make_float2(d, s);
+  float d, sum;
+  const signed char c = q8_1_lane(i < n ? x[i] : 0.0f, d, sum);
+  if (i < n) q[i] = c;
+  if (i < n && (threadIdx.x & 31) == 0) ds[i >> 5] = make_float2(d, sum);
 }
 
 int launch_q8_1(const float* x, uint32_t n, int8_t* q, float2* ds, hipStream_t st) {
@@ -111,146 +106,40 @@ int launch_group(const uint32_t* ids, uint32_t n, uint32_t nk, uint32_t ne, uint
   return 0;
 }
 
-// ---------------------------------------------------------------- block dots
-
-DEV int dot4(u32 a, u32 b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
-
-// 32-column block b of a row against 32 int8 x (8 dwords) with {d, s}
-template <u32 F> DEV float blk_q8(const u8* row, u32 b, const u32* xq, float2 e);
-
-template <> __device__ __forceinline__ float blk_q8<FM_Q4_K>(const u8* row, u32 b, const u32* xq, float2 e) {
-  const u8* B = row + (u64)(b >> 3) * 144u;
-  const u32 j = b & 7u;
-  const uint4 h = *(const uint4*)B;
-  const uint4* qp = (const uint4*)(B + 16 + 32 * (j >> 1));
-  const uint4 q0 = qp[0], q1 = qp[1];
-  const u32 q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-  const u32 sh = 4u * (j & 1u);
-  int acc = 0;
-#pragma unroll
-  for (int k = 0; k < 8; k++) acc = dot4((q[k] >> sh) & 0x0F0F0F0Fu, xq[k], acc);
-  u32 sc, mn;
-  k4_scmin(h, j, sc, mn);
-  return f16v(h.x & 0xffffu) * (float)sc * e.x * (float)acc - f16v(h.x >> 16) * (float)mn * e.y;
-}
-template <> __device__ __forceinline__ float blk_q8<FM_Q5_K>(const u8* row, u32 b, const u32* xq, float2 e) {
-  const u8* B = row + (u64)(b >> 3) * 176u;
-  const u32 j = b & 7u;
-  const uint4 h = *(const uint4*)B;
-  const uint4 h0 = *(const uint4*)(B + 16), h1 = *(const uint4*)(B + 32);
-  const uint4* qp = (const uint4*)(B + 48 + 32 * (j >> 1));
-  const uint4 q0 = qp[0], q1 = qp[1];
-  const u32 q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-  const u32 qh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-  const u32 sh = 4u * (j & 1u);
-  int acc = 0;
-#pragma unroll
-  for (int k = 0; k < 8; k++) acc = dot4(((q[k] >> sh) & 0x0F0F0F0Fu) | (((qh[k] >> j) & 0x01010101u) << 4), xq[k], acc);
-  u32 sc, mn;
-  k4_scmin(h, j, sc, mn);
-  return f16v(h.x & 0xffffu) * (float)sc * e.x * (float)acc - f16v(h.x >> 16) * (float)mn * e.y;
-}
-template <> __device__ __forceinline__ float blk_q8<FM_Q6_K>(const u8* row, u32 b, const u32* xq, float2 e) {
-  const u8* B = row + (u64)(b >> 3) * 210u;
-  const u32 bb = b & 7u, n = bb >> 2, quad = bb & 3u;
-  u32 ql[8], qh[8];
-  ld32_a2(B + 64 * n + 32 * (quad & 1u), ql);
-  ld32_a2(B + 128 + 32 * n, qh);
-  const u32 nsh = quad >= 2u ? 4u : 0u, hsh = 2u * quad;
-  int a0 = 0, a1 = 0;
-#pragma unroll
-  for (int k = 0; k < 8; k++) {
-    const u32 v = ((ql[k] >> nsh) & 0x0F0F0F0Fu) | (((qh[k] >> hsh) & 0x03030303u) << 4);
-    const u32 c = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;  // per byte q - 32, signed
-    if (k < 4) a0 = dot4(c, xq[k], a0);
-    else a1 = dot4(c, xq[k], a1);
-  }
-  const u32 scw = ld_u16(B + 192 + 8 * n + 2 * quad);
-  const float d = f16v(ld_u16(B + 208));
-  return d * e.x * ((float)(int)(signed char)(scw & 255u) * (float)a0 + (float)(int)(signed char)(scw >> 8) * (float)a1);
-}
-template <> __device__ __forceinline__ float blk_q8<FM_Q8_0>(const u8* row, u32 b, const u32* xq, float2 e) {
-  const u8* B = row + (u64)b * 34u;
-  const u32* a = al4(B);
-  const bool odd = ((uintptr_t)B & 2u) != 0;
-  u32 v[9];
-#pragma unroll
-  for (int k = 0; k < 9; k++) v[k] = a[k];
-  int acc = 0;
-#pragma unroll
-  for (int k = 0; k < 8; k++) acc = dot4(odd ? v[k + 1] : __builtin_amdgcn_alignbit(v[k + 1], v[k], 16), xq[k], acc);
-  return f16v(odd ? v[0] >> 16 : v[0] & 0xffffu) * e.x * (float)acc;
-}
-
-// a row's q8 dot on the 4 lanes of a lane group: lane p takes blocks p, p + 4, ...
-template <u32 F>
-DEV float row_q8(const u8* row, u32 cols, const signed char* xq, const float2* xd, u32 p) {
-  float acc = 0.0f;
-  for (u32 b = p; b < cols / 32; b += 4) {
-    const uint4 a0 = *(const uint4*)(xq + 32 * b), a1 = *(const uint4*)(xq + 32 * b + 16);
-    const u32 x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    acc += blk_q8<F>(row, b, x, xd[b]);
-  }
-  acc += __shfl_xor(acc, 2, 64);
-  acc += __shfl_xor(acc, 1, 64);
-  return acc;
-}
-DEV float row_q8_fm(u32 f, const u8* row, u32 cols, const signed char* xq, const float2* xd, u32 p) {
-  switch (f) {
-    case FM_Q8_0: return row_q8<FM_Q8_0>(row, cols, xq, xd, p);
-    case FM_Q4_K: return row_q8<FM_Q4_K>(row, cols, xq, xd, p);
-    case FM_Q6_K: return row_q8<FM_Q6_K>(row, cols, xq, xd, p);
-    default: return row_q8<FM_Q5_K>(row, cols, xq, xd, p);
-  }
-}
-
 // ---------------------------------------------------------------- decode-shaped kernels (per slot)
 
-// gate + up + SwiGLU for each (token, rank) slot: 128 threads = 16 row pairs of one slot;
-// shared expert rows ride along as slot index T nk + t (its own weights, x of token t)
-__global__ void __launch_bounds__(128) k_gu_q8(Q8Args a, u32 nslot) {
-  const u32 task0 = blockIdx.x * 16;
-  const u32 L = threadIdx.x & 63, q = L >> 2, p = L & 3;
-  const u32 pr = 8 * (threadIdx.x >> 6) + (q & 7);
-  u32 slot, row, t, cols = a.dm;
-  const u8* w;
-  u32 f;
-  float* out;
-  if (task0 < nslot * a.ef) {
-    slot = task0 / a.ef;
-    row = task0 % a.ef + pr;
-    t = slot / a.nk;
-    const u64 e = a.ids[slot];
-    w = q < 8 ? a.G + e * a.es + row * a.rbg : a.U + e * a.es + row * a.rbu;
-    f = q < 8 ? a.fg : a.fu;
-    out = a.act + (u64)slot * a.ef + row;
-  } else {
-    const u32 k = task0 - nslot * a.ef;
-    t = k / a.sf;
-    row = k % a.sf + pr;
-    w = q < 8 ? a.SG + (u64)row * a.rbsg : a.SU + (u64)row * a.rbsu;
-    f = q < 8 ? a.fsg : a.fsu;
-    out = a.sa + (u64)t * a.sf + row;
-  }
-  const float v = row_q8_fm(f, w, cols, a.hq + (u64)t * a.dm, a.hd + (u64)t * (a.dm / 32), p);
-  const float u = __shfl_xor(v, 32, 64);
-  if (q < 8 && p == 0) *out = silu_mul(v, u);
-}
-
-// down + combine (llb_mx_dn + llb_mx_comb): rw rows of token blockIdx.y, tasks (j, r)
-__global__ void __launch_bounds__(256) k_dn_q8(Q8Args a) {
-  __shared__ float part[64];
+// down + combine (llb_mx_dn + llb_mx_comb): rw rows of token blockIdx.y, tasks (j, r). With lq (few
+// tokens) the block quantizes its token's act and shared activations to q8_1 in LDS itself -- the
+// same q8_1_lane steps as k_q8_1, so the same bits -- instead of a launch of k_q8_1 before it.
+__global__ void __launch_bounds__(256) k_dn_q8(Q8Args a, u32 lq) {
+  extern __shared__ float4 dsm[];  // part [64]; with lq: aq [nk ef], sq [sf], ad [nk ef / 32], sd [sf / 32]
+  float* part = (float*)dsm;
   const u32 t = blockIdx.y, nt = a.nk + (a.sf ? 1u : 0u);
+  // act in LDS or in memory: separate call sites keep each pointer's address space (no flat loads)
+  const u32 na = a.nk * a.ef;
+  signed char* laq = (signed char*)(part + 64);
+  signed char* lsq = laq + na;
+  float2* lad = (float2*)(lsq + a.sf);
+  float2* lsd = lad + na / 32;
+  if (lq) {
+    q8_1_block256<32>(a.act + (u64)t * na, na, laq, lad);
+    if (a.sf) q8_1_block256<16>(a.sa + (u64)t * a.sf, a.sf, lsq, lsd);
+    __syncthreads();
+  }
   const u32 g = threadIdx.x >> 2, p = threadIdx.x & 3;
   if (g < a.rw * nt) {
     const u32 j = g / a.rw, rl = g % a.rw, r = blockIdx.x * a.rw + rl;
     if (r < a.dm) {
       float v;
       if (j < a.nk) {
-        const u64 slot = (u64)t * a.nk + j, e = a.ids[slot];
-        v = row_q8_fm(a.fd, a.D + (e * a.dm + r) * a.rbd, a.ef, a.aq + slot * a.ef, a.ad + slot * (a.ef / 32), p);
+        const u64 e = a.ids[(u64)t * a.nk + j];
+        const u8* row = a.D + (e * a.dm + r) * a.rbd;
+        if (lq) v = row_q8_fm(a.fd, row, a.ef, laq + (u64)j * a.ef, lad + (u64)j * (a.ef / 32), p);
+        else v = row_q8_fm(a.fd, row, a.ef, a.aq + ((u64)t * a.nk + j) * a.ef, a.ad + ((u64)t * a.nk + j) * (a.ef / 32), p);
       } else {
-        v = row_q8_fm(a.fsd, a.SD + (u64)r * a.rbs, a.sf, a.sq + (u64)t * a.sf, a.sd2 + (u64)t * (a.sf / 32), p);
+        const u8* row = a.SD + (u64)r * a.rbs;
+        if (lq) v = row_q8_fm(a.fsd, row, a.sf, lsq, lsd, p);
+        else v = row_q8_fm(a.fsd, row, a.sf, a.sq + (u64)t * a.sf, a.sd2 + (u64)t * (a.sf / 32), p);
       }
       if (p == 0) part[g] = v;
     }
@@ -285,8 +174,12 @@ size_t moe_q8_scratch(const llb_moe_layer* L, uint32_t T) {
          al(n * L->ef / 32 * 8) + al((size_t)T * L->sf * 4 + 4) + al((size_t)T * L->sf + 4) + al((size_t)T * L->sf / 32 * 8 + 8);
 }
 
+// few tokens: each kernel quantizes the activations it reads in LDS (no q8_1 launches); more: the
+// q8_1 launches, once for all blocks
+#define Q8_LOCAL_T 8u
+
 int moe_q8_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const float* x1, float* y, const uint32_t* ids,
-                   const float* wt, const float* sgo, uint8_t* sc, hipStream_t st) {
+                   const float* wt, const float* sgo, const TopkArgs* tk, uint8_t* sc, hipStream_t st) {
   const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
   Q8Args a{};
   const size_t n = (size_t)T * L->nk;
@@ -320,17 +213,28 @@ int moe_q8_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const fl
   a.x1 = x1;
   a.y = y;
   a.sgo = sgo;
-  stage_begin(ST_Q8X);
-  launch_q8_1(h2, T * L->dm, (int8_t*)a.hq, (float2*)a.hd, st);
-  stage_end(ST_Q8X);
-  const uint32_t tasks = (uint32_t)(n * L->ef + (size_t)T * L->sf) / 16;
+  // (the in-LDS quantizers hold 16 / 32 values a thread: dm, sf <= 4096, nk ef <= 8192)
+  const bool lq = T <= Q8_LOCAL_T && L->dm <= 4096 && (size_t)L->nk * L->ef <= 8192 && L->sf <= 4096;
+  // top-k inside the gate / up launch takes one token
+  if (tk && (T != 1 || !lq)) return -1;
+  if (!lq) {
+    stage_begin(ST_Q8X);
+    launch_q8_1(h2, T * L->dm, (int8_t*)a.hq, (float2*)a.hd, st);
+    stage_end(ST_Q8X);
+  }
+  a.h2 = h2;
   stage_begin(ST_GU);
-  LAUNCH_K(k_gu_q8, dim3(tasks), dim3(128), 0, st, a, (u32)n);
+  int rc = launch_gu_q8(a, tk, (u32)n, T, lq, st);
   stage_end(ST_GU);
-  launch_q8_1(a.act, (uint32_t)(n * L->ef), a.aq, a.ad, st);
-  if (L->sf) launch_q8_1(a.sa, T * L->sf, a.sq, a.sd2, st);
+  if (rc) return rc;
+  if (!lq) {
+    launch_q8_1(a.act, (uint32_t)(n * L->ef), a.aq, a.ad, st);
+    if (L->sf) launch_q8_1(a.sa, T * L->sf, a.sq, a.sd2, st);
+  }
+  const size_t lsm = 256 + (lq ? (size_t)L->nk * L->ef * 5 / 4 + (size_t)L->sf * 5 / 4 : 0);
+  if (lsm > 65536) return -1;
   stage_begin(ST_DN);
-  LAUNCH_K(k_dn_q8, dim3((L->dm + a.rw - 1) / a.rw, T), dim3(256), 0, st, a);
+  LAUNCH_K(k_dn_q8, dim3((L->dm + a.rw - 1) / a.rw, T), dim3(256), lsm, st, a, (u32)lq);
   stage_end(ST_DN);
   return 0;
 }

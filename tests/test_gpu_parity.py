@@ -206,7 +206,7 @@ def test_q8_1_matches_oracle(dev):
     assert np.allclose(gds[:, 1], rs, rtol=1e-5, atol=1e-5)
 
 
-@pytest.mark.parametrize("name,T", [("c2", 1), ("c1", 4), ("c2", 8)])
+@pytest.mark.parametrize("name,T", [("c2", 1), ("c1", 4), ("c2", 8), ("c1", 16)])
 def test_q8_tier_tolerance(dev, name, T):
     shape = em.SHAPES[name]
     _say("q8", name, T)
@@ -227,6 +227,26 @@ def test_q8_tier_tolerance(dev, name, T):
     m64 = ol.err_metrics(y, hl.f64(h2, ids))
     _say("q8 vs float64", m64)
     assert m64["cos"] >= 0.999
+
+
+def test_q8_tier_same_bits_every_path(dev):
+    """the q8 tier's three launch shapes give the same bits token for token: one token (top-k inside the
+    gate / up launch, activations quantized in LDS), eight tokens (quantized in LDS), nine tokens (the
+    q8_1 launches)"""
+    shape = em.SHAPES["c2"]
+    layer = em.Layer(dev, shape, seed=4)
+    ys = {}
+    for T in (1, 8, 9):
+        _say("q8 paths", "T", T)
+        run = em.Runner(dev, shape, T, tier=em.Q8)
+        run.gen_inputs(4)
+        run.forward(layer)
+        ys[T] = run.outputs()
+        run.free()
+    layer.free()
+    for a, b, n in ((1, 9, 1), (8, 9, 8)):
+        for u, v in zip(ys[a], ys[b]):
+            assert np.array_equal(np.asarray(u[:n]).view(np.uint32), np.asarray(v[:n]).view(np.uint32)), (a, b)
 
 
 def _nan_equal(a, b):
