@@ -336,6 +336,30 @@ static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* 
 static int fused_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const float* x1, float* y, uint32_t* ids,
                          float* wt, uint8_t* sc, const ExactScratch& s);
 
+// A second stream for work that overlaps the routed experts' GEMMs (the shared expert's), one per
+// device, default priority, with a fork / join event pair. fork: the side stream waits for everything
+// queued on the library's stream so far; join: the library's stream waits for the side stream. Both are
+// event edges, so a graph capture records them (the side stream joins the capture and is joined back).
+struct Side {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+static Side g_side[64];
+static int side_get(Side** out) {
+  int d = 0;
+  int rc = hip_ok(hipGetDevice(&d), "hipGetDevice");
+  if (rc) return rc;
+  if (d < 0 || d >= 64) return fail(LLB_HIP_EINVAL, "device %d: at most 64 devices", d);
+  Side& x = g_side[d];
+  if (!x.s) {
+    if ((rc = hip_ok(hipStreamCreateWithFlags(&x.s, hipStreamNonBlocking), "side hipStreamCreate"))) return rc;
+    if ((rc = hip_ok(hipEventCreateWithFlags(&x.fork, hipEventDisableTiming), "side hipEventCreate"))) return rc;
+    if ((rc = hip_ok(hipEventCreateWithFlags(&x.join, hipEventDisableTiming), "side hipEventCreate"))) return rc;
+  }
+  *out = &x;
+  return 0;
+}
+
 // the grouped-GEMM tier: exact routing, the dispatch permutation, expert GEMMs on MFMA, combine
 static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const float* x1, float* y, uint32_t* ids,
                         float* wt, uint8_t* sc, const ExactScratch& s) {
@@ -358,6 +382,44 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
                      "group + f16 activations")))
     return rc;
   stage_end(ST_Q8X);
+  // the shared expert (dense over the T tokens) needs only x16: on the side stream, overlapping the
+  // routed GEMMs, which leave most of the chip idle at a few hundred tokens
+  const float* shd = nullptr;
+  Side* side = nullptr;
+  if (L->sf) {
+    if ((rc = side_get(&side))) return rc;
+    if ((rc = hip_ok(hipEventRecord(side->fork, g_stream), "fork hipEventRecord"))) return rc;
+    if ((rc = hip_ok(hipStreamWaitEvent(side->s, side->fork, 0), "fork hipStreamWaitEvent"))) return rc;
+    const uint32_t mt = (T + gemm_bm() - 1) / gemm_bm();
+    GemmArgs sg{};
+    sg.W0 = dp<uint8_t>(L->SG);
+    sg.W1 = dp<uint8_t>(L->SU);
+    sg.rb = row_bytes(L->fsg, L->dm);
+    sg.K = L->dm;
+    sg.N = L->sf;
+    sg.M = T;
+    sg.A = x16;
+    sg.arows = T;
+    sg.out = gb + gs.sact;
+    if (L->PSG && L->PSU) {
+      sg.P0 = dp<uint8_t>(L->PSG);
+      sg.P1 = dp<uint8_t>(L->PSU);
+    }
+    if ((rc = launched(launch_moe_gemm(sg, L->fsg, 0, mt, side->s), "shared gate/up GEMM"))) return rc;
+    GemmArgs sd{};
+    sd.W0 = dp<uint8_t>(L->SD);
+    sd.rb = row_bytes(L->fsd, L->sf);
+    sd.K = L->sf;
+    sd.N = L->dm;
+    sd.M = T;
+    sd.A = (const _Float16*)(gb + gs.sact);
+    sd.arows = T;
+    sd.out = gb + gs.shd;
+    sd.P0 = L->PSD ? dp<uint8_t>(L->PSD) : nullptr;
+    if ((rc = launched(launch_moe_gemm(sd, L->fsd, 1, mt, side->s), "shared down GEMM"))) return rc;
+    if ((rc = hip_ok(hipEventRecord(side->join, side->s), "join hipEventRecord"))) return rc;
+    shd = (const float*)(gb + gs.shd);
+  }
   const uint64_t rbg = row_bytes(fg, L->dm), rbd = row_bytes(fd, L->ef);
   const uint32_t maxt = n / gemm_bm() + L->ne + 1;  // >= sum over experts of ceil(M_e / BM)
   GemmArgs g{};
@@ -398,37 +460,7 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
   stage_begin(ST_DN);
   if ((rc = launched(launch_moe_gemm(d, fd, 1, maxt, g_stream), "expert down GEMM"))) return rc;
   stage_end(ST_DN);
-  const float* shd = nullptr;
-  if (L->sf) {
-    const uint32_t mt = (T + gemm_bm() - 1) / gemm_bm();
-    GemmArgs sg{};
-    sg.W0 = dp<uint8_t>(L->SG);
-    sg.W1 = dp<uint8_t>(L->SU);
-    sg.rb = row_bytes(L->fsg, L->dm);
-    sg.K = L->dm;
-    sg.N = L->sf;
-    sg.M = T;
-    sg.A = x16;
-    sg.arows = T;
-    sg.out = gb + gs.sact;
-    if (L->PSG && L->PSU) {
-      sg.P0 = dp<uint8_t>(L->PSG);
-      sg.P1 = dp<uint8_t>(L->PSU);
-    }
-    if ((rc = launched(launch_moe_gemm(sg, L->fsg, 0, mt, g_stream), "shared gate/up GEMM"))) return rc;
-    GemmArgs sd{};
-    sd.W0 = dp<uint8_t>(L->SD);
-    sd.rb = row_bytes(L->fsd, L->sf);
-    sd.K = L->sf;
-    sd.N = L->dm;
-    sd.M = T;
-    sd.A = (const _Float16*)(gb + gs.sact);
-    sd.arows = T;
-    sd.out = gb + gs.shd;
-    sd.P0 = L->PSD ? dp<uint8_t>(L->PSD) : nullptr;
-    if ((rc = launched(launch_moe_gemm(sd, L->fsd, 1, mt, g_stream), "shared down GEMM"))) return rc;
-    shd = (const float*)(gb + gs.shd);
-  }
+  if (side && (rc = hip_ok(hipStreamWaitEvent(g_stream, side->join, 0), "join hipStreamWaitEvent"))) return rc;
   return launched(launch_combine((const float*)(gb + gs.out), inv, wt, L->nk, shd, (const float*)(sc + s.sgo), x1, y,
                                  L->dm, T, g_stream),
                   "combine");

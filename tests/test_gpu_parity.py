@@ -249,6 +249,36 @@ def test_q8_tier_same_bits_every_path(dev):
             assert np.array_equal(np.asarray(u[:n]).view(np.uint32), np.asarray(v[:n]).view(np.uint32)), (a, b)
 
 
+@pytest.mark.parametrize("name,T,tier", [("c2", 1, em.EXACT), ("c2", 1, em.Q8), ("c2", 40, em.F16), ("c5", 33, em.F16)])
+def test_graph_replays_match_eager(dev, name, T, tier):
+    """a captured layer (llb_hip_graph_begin / end) replayed three times, with an eager forward of another
+    layer between the replays (it overwrites y, ids, wt and the scratch), gives the eager result's bits
+    every time -- including the f16 tier's shared expert, which runs on a side stream forked and joined
+    by events inside the capture"""
+    shape = em.SHAPES[name]
+    _say("graph replays", name, "T", T, "tier", tier)
+    layer, other = em.Layer(dev, shape, seed=6), em.Layer(dev, shape, seed=7)
+    run = em.Runner(dev, shape, T, tier=tier)
+    run.gen_inputs(6)
+    run.forward(layer)
+    ref = run.outputs()
+    h = dev.capture(lambda: run.forward(layer))
+    try:
+        for rep in range(3):
+            run.forward(other)
+            dev.sync()
+            dev.replay(h)
+            dev.sync()
+            got = run.outputs()
+            for a, b in zip(got, ref):
+                assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32)), rep
+    finally:
+        dev.check(dev.lib.llb_hip_graph_free(h))
+        run.free()
+        layer.free()
+        other.free()
+
+
 def _nan_equal(a, b):
     a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
     ok = (np.isnan(a) & np.isnan(b)) | (a.view(np.uint32) == b.view(np.uint32))
