@@ -32,7 +32,7 @@ int launch_q8_1(const float* x, uint32_t n, int8_t* q, float2* ds, hipStream_t s
 // block e of ne: off[e] = #{slots with id < e}; then e's slots in ascending slot order, each
 // wave's ballot giving a slot its rank: xmap[pos] = slot / nk, inv[slot] = pos. Deterministic.
 // the dispatch permutation (llb_mx_group, host/llb_pf.cuh:774-817): slots of expert e in slot order.
-// Block e; thread t scans the contiguous slots [t per, t per + per): ids below e (the expert's offset)
+// Block e; thread t scans its contiguous slots: ids below e (the expert's offset)
 // and equal to e (its hits); an exclusive scan of the hits over the block gives each thread its first
 // position, and it writes its hits in slot order -- the stable order, with one scan a block.
 // Blocks past ne (when x16 is set) convert the activations to f16 for the grouped GEMM instead, 8
@@ -53,20 +53,41 @@ __global__ void __launch_bounds__(256) k_group(const u32* __restrict__ ids, u32 
     return;
   }
   const u32 e = blockIdx.x, t = threadIdx.x, w = t >> 6, L = t & 63;
-  const u32 per = (n + 255) / 256, i0 = min(t * per, n), i1 = min(i0 + per, n);
-  u32 lt = 0, hit = 0, i = i0;
-  if (per % 4 == 0 && ((uintptr_t)ids & 15) == 0) {  // whole uint4s from i0 (i0 = t per), loads in flight together
-#pragma unroll 4
-    for (; i + 4 <= i1; i += 4) {
-      const uint4 v = *(const uint4*)(ids + i);
-      lt += (v.x < e ? 1u : 0u) + (v.y < e ? 1u : 0u) + (v.z < e ? 1u : 0u) + (v.w < e ? 1u : 0u);
-      hit += (v.x == e ? 1u : 0u) + (v.y == e ? 1u : 0u) + (v.z == e ? 1u : 0u) + (v.w == e ? 1u : 0u);
+  // thread t scans the contiguous slots [t per, t per + per), per a multiple of 4 (16-byte loads)
+  const u32 per = ((n + 255) / 256 + 3) & ~3u, i0 = min(t * per, n), i1 = min(i0 + per, n);
+  // up to 64 slots a thread: all its ids in registers from one round of loads, reused by the scatter
+  // below; a partial last quad holds ~0 past n (never an expert: it counts neither below nor at e)
+  const bool reg = per <= 64 && ((uintptr_t)ids & 15) == 0;
+  uint4 v[16];
+  u32 lt = 0, hit = 0;
+  if (reg) {
+#pragma unroll
+    for (u32 q = 0; q < 16; q++) {
+      const u32 i = i0 + 4 * q;
+      uint4 x = make_uint4(~0u, ~0u, ~0u, ~0u);
+      if (4 * q < per && i < i1) {
+        if (i + 4 <= i1) {
+          x = *(const uint4*)(ids + i);
+        } else {
+          x.x = ids[i];
+          if (i + 1 < i1) x.y = ids[i + 1];
+          if (i + 2 < i1) x.z = ids[i + 2];
+        }
+      }
+      v[q] = x;
     }
-  }
-  for (; i < i1; i++) {
-    const u32 v = ids[i];
-    lt += v < e ? 1u : 0u;
-    hit += v == e ? 1u : 0u;
+#pragma unroll
+    for (u32 q = 0; q < 16; q++) {
+      const uint4 x = v[q];
+      lt += (x.x < e ? 1u : 0u) + (x.y < e ? 1u : 0u) + (x.z < e ? 1u : 0u) + (x.w < e ? 1u : 0u);
+      hit += (x.x == e ? 1u : 0u) + (x.y == e ? 1u : 0u) + (x.z == e ? 1u : 0u) + (x.w == e ? 1u : 0u);
+    }
+  } else {
+    for (u32 i = i0; i < i1; i++) {
+      const u32 x = ids[i];
+      lt += x < e ? 1u : 0u;
+      hit += x == e ? 1u : 0u;
+    }
   }
   // inclusive scan of hit across the wave, sum of lt
   u32 inc = hit, lsum = lt;
@@ -86,7 +107,21 @@ __global__ void __launch_bounds__(256) k_group(const u32* __restrict__ ids, u32 
     off[e] = base;
     if (e + 1 == ne) off[ne] = n;
   }
-  if (hit) {
+  if (hit && reg) {
+#pragma unroll
+    for (u32 q = 0; q < 16; q++) {
+      const u32 xs[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+      for (u32 c = 0; c < 4; c++) {
+        if (xs[c] == e) {  // only slots below i1 can hold e
+          const u32 i = i0 + 4 * q + c;
+          xmap[pos] = i / nk;
+          inv[i] = pos;
+          pos++;
+        }
+      }
+    }
+  } else if (hit) {
     for (u32 i = i0; i < i1; i++) {
       if (ids[i] == e) {
         xmap[pos] = i / nk;

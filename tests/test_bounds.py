@@ -79,3 +79,27 @@ def test_the_fixed_q8_0_over_read_is_caught():
     cols = 2048
     row = cols // 32 * 34
     assert max(hi for c in range(0, cols, 32) for jh in (0, 1) for _, hi in old_half_q8(c, jh)) == row + 2
+
+
+# k_group's slot chunks (csrc/moe_q8.hip): thread t of 256 scans [t per, t per + per) with per rounded up to
+# a multiple of 4; with per <= 64 its ids come through 16 quads, whole 16-byte loads only when the quad lies
+# inside [i0, i1), single words for a ragged last quad
+@pytest.mark.parametrize("n", [0, 1, 3, 8, 512, 513, 5130, 16384, 16385, 40000])
+def test_group_chunks_in_range(n):
+    per = ((n + 255) // 256 + 3) & ~3
+    assert per % 4 == 0
+    covered = []
+    for t in range(256):
+        i0 = min(t * per, n)
+        i1 = min(i0 + per, n)
+        covered.extend(range(i0, i1))
+        if per <= 64:
+            for q in range(16):
+                i = i0 + 4 * q
+                if not (4 * q < per and i < i1):
+                    continue
+                if i + 4 <= i1:
+                    assert i % 4 == 0 and i + 4 <= n       # an aligned whole quad inside the ids
+                else:
+                    assert all(j < n for j in range(i, i1))  # the ragged tail: words below i1 only
+    assert covered == list(range(n))                      # every slot once, in slot order
