@@ -136,6 +136,49 @@ def test_topk_kernel_ties_and_full(dev):
     assert list(gi[1]) == [6, 13, 20, 27, 34]
 
 
+def test_topk_nonfinite_logits_keep_ids_in_range(dev):
+    """NaN and infinite logits: the reference's ranking is undefined there (NaN compares false; an inf
+    makes every p NaN), but every id the kernel writes must still name an expert, since the expert
+    kernels address weights with it"""
+    ne, nk = 256, 8
+    rng = np.random.default_rng(3)
+    lg = rng.standard_normal((6, ne + 1)).astype(np.float32)
+    lg[0, :ne] = np.nan                       # all NaN
+    lg[1, 1:ne:2] = np.nan                    # every other NaN
+    lg[2, 17] = np.inf                        # one +inf
+    lg[3, :ne] = -np.inf                      # all -inf
+    lg[4, :ne - 3] = np.nan                   # fewer finite logits than nk
+    lg[5, ::3] = -np.inf
+    lg[5, 1::3] = np.inf
+    p = dev.upload(lg)
+    ids, wt, sgo = dev.alloc(6 * nk * 4), dev.alloc(6 * nk * 4), dev.alloc(24)
+    dev.check(dev.lib.llb_moe_hip_topk(p, ne + 1, 6, ne, nk, 1, ids, wt, sgo))
+    gi = dev.read(ids, (6, nk), np.uint32)
+    assert (gi < ne).all(), gi
+    # one NaN logit makes the softmax sum NaN, so every p is NaN and no expert ranks: each slot keeps
+    # expert 0 (a valid address)
+    assert (gi[[0, 1, 4]] == 0).all()
+
+
+def test_forward_nonfinite_input_keeps_ids_in_range(dev):
+    """a NaN in the FFN input makes every logit NaN: each tier still routes to valid experts and
+    returns (no fault, no error), with NaN outputs"""
+    shape, T = em.SHAPES["c2"], 4
+    layer = em.Layer(dev, shape, seed=8)
+    for tier in (em.EXACT, em.Q8, em.F16):
+        run = em.Runner(dev, shape, T, tier=tier)
+        x = np.random.default_rng(8).standard_normal((T, shape.dm)).astype(np.float32)
+        x[1, 5] = np.nan
+        x[2, 9] = np.inf
+        dev.check(dev.lib.llb_hip_write(run.h2, x.ctypes.data, x.nbytes))
+        run.forward(layer, residual=False)
+        y, ids, wt = run.outputs()
+        run.free()
+        assert (ids < shape.ne).all(), (tier, ids)
+        assert np.isfinite(y[0]).all() and np.isfinite(y[3]).all()   # the finite tokens are untouched
+    layer.free()
+
+
 @pytest.mark.parametrize("ne,nk", [(256, 8), (1024, 63), (64, 1), (1000, 10), (513, 5), (130, 64)])
 def test_topk_kernel_patterns(dev, ne, nk):
     """Tie patterns around the kernel's candidate pruning (the nk-th largest of 64 strided maxima):
