@@ -356,8 +356,9 @@ def main():
     ap.add_argument("--prefill-T", type=int, default=2048)
     ap.add_argument("--no-c5", dest="c5", action="store_false",
                     help="skip the config-5 leg (48 resident 512-expert layers, 1 + 512 tokens a launch)")
-    ap.add_argument("--legs", default="q8,batched,prefill,prefill_k,c5,rmsnorm,residency,copy",
-                    help="legs after the decode line: q8 (the int8 tier's decode), batched (config 3), prefill (c1), "
+    ap.add_argument("--legs", default="q8,step,batched,prefill,prefill_k,c5,rmsnorm,residency,copy",
+                    help="legs after the decode line: q8 (the int8 tier's decode), step (the decode step with the "
+                         "input step, two calls or one), batched (config 3), prefill (c1), "
                          "prefill_k (c1k), c5, rmsnorm, residency (GGUF stacks in each residency mode), copy "
                          "(achievable HBM bandwidth)")
     ap.add_argument("--traffic-from", metavar="DIR",
@@ -461,6 +462,49 @@ def main():
         q8_us = (time.perf_counter() - t0) / (args.steps * args.layers) * 1e6
         dev.free(sc8)
 
+    # a whole decode step per layer: the input step (x1 = x + z, h2 = rmsnorm(x1) w) then the layer, each
+    # layer's input the previous layer's output, one HIP graph a step; two calls a layer, and the input
+    # step inside the router launch (llb_moe_hip_forward_norm)
+    step_us = None
+    if "step" in legs and tier == em.EXACT:
+        z = dev.alloc(shape.dm * 4)
+        wn = dev.alloc(shape.dm * 4)
+        xin = dev.alloc(shape.dm * 4)
+        dev.check(dev.lib.llb_moe_hip_gen_gauss(1, em.ST_X1, 0, shape.dm, 1.0, z))
+        dev.check(dev.lib.llb_moe_hip_gen_gauss(1, em.ST_H2, 0, shape.dm, 1.0, xin))
+        dev.check(dev.lib.llb_moe_hip_gen_gauss(2, 0, 0, shape.dm, 0.1, wn))
+        dm4 = shape.dm * 4
+
+        def chain(fused):
+            def f():
+                for i, L in enumerate(layers):
+                    xi = xin if i == 0 else y + (i - 1) * dm4
+                    a = (C.byref(L.desc), T)
+                    tail = (y + i * dm4, ids + i * shape.nk * 4, wt + i * shape.nk * 4, sc, sb, tier)
+                    if fused:
+                        dev.check(dev.lib.llb_moe_hip_forward_norm(*a, xi, z, wn, 1e-6, x1 + i * dm4, h2 + i * dm4, *tail))
+                    else:
+                        dev.check(dev.lib.llb_moe_hip_rmsnorm_add(xi, z, wn, 1e-6, T, shape.dm, x1 + i * dm4, h2 + i * dm4))
+                        dev.check(dev.lib.llb_moe_hip_forward(*a, h2 + i * dm4, x1 + i * dm4, *tail))
+            return f
+        step_us = {}
+        for nm, fused in (("two_calls", False), ("input_step_in_router", True)):
+            fn = chain(fused)
+            gs = dev.capture(fn) if args.graph else None
+            runs = (lambda: dev.replay(gs)) if args.graph else fn
+            for _ in range(args.warmup):
+                runs()
+            dev.sync()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                runs()
+            dev.sync()
+            step_us[nm] = round((time.perf_counter() - t0) / (args.steps * args.layers) * 1e6, 3)
+            if gs:
+                dev.check(dev.lib.llb_hip_graph_free(gs))
+        for p_ in (z, wn, xin):
+            dev.free(p_)
+
     sbytes = stage_bytes(shape)
     dom = max(("gate_up", "down"), key=lambda k: stages.get(k, (0, 0))[0])
     dom_us = stages[dom][0]
@@ -487,6 +531,11 @@ def main():
                      "traffic": measured_traffic(f"{args.config}_decode", dom, args.tier == "exact"),
                      "bytes_per_launch": sbytes[dom], "kernel_us": round(dom_us, 3)},
     }
+    if step_us is not None:
+        out["decode_step_with_input"] = dict(us_per_token_layer=step_us, config=(
+            f"{args.config} decode, 1 token a layer through {args.layers} layers, each layer's input step "
+            f"(llb_rmsnorm_add, eps 1e-6) then the layer, the next layer's input its output; exact tier"
+            f"{', one HIP graph a step' if args.graph else ''}"))
     if q8_us is not None:
         out["decode_q8_tier"] = {"us_per_token_layer": round(q8_us, 3),
                                  "config": f"{args.config} decode, the int8 tier (q8_1 activations, v_dot4), same layers "

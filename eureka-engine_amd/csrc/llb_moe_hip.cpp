@@ -291,8 +291,15 @@ size_t llb_moe_hip_scratch_bytes(const llb_moe_layer* L, uint32_t T, int tier) {
 // router + shared gate logit + shared gate / up (the tree rows), then top-k and sa
 // the router / shared rows launch, then top-k -- or, with defer, top-k's arguments for a later
 // launch that routes in-kernel
+// the input step riding on the router launch (llb_moe_hip_forward_norm): x, z, w, eps in; x1, h2 out
+struct NormIn {
+  const float *x, *z, *w;
+  float eps;
+  float *x1, *h2;
+};
 static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* ids, float* wt, uint8_t* sc,
-                 const ExactScratch& s, bool shared_rows = true, TopkArgs* defer = nullptr) {
+                 const ExactScratch& s, bool shared_rows = true, TopkArgs* defer = nullptr,
+                 const NormIn* nin = nullptr) {
   float* lg = (float*)(sc + s.lg);
   float* gsu = (float*)(sc + s.gsu);
   TreeArgs a{};
@@ -309,6 +316,14 @@ static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* 
   a.seg[2] = TreeSeg{dp<uint8_t>(L->SG), L->fsg, row_bytes(L->fsg, L->dm), L->sf, gsu, 2 * L->sf, nullptr};
   a.seg[3] = TreeSeg{dp<uint8_t>(L->SU), L->fsu, row_bytes(L->fsu, L->dm), L->sf, gsu + L->sf, 2 * L->sf, nullptr};
   a.nseg = shared_rows ? 4 : 2;
+  if (nin) {
+    a.x = nin->x;
+    a.nz = nin->z;
+    a.nw = nin->w;
+    a.eps = nin->eps;
+    a.x1o = nin->x1;
+    a.h2o = nin->h2;
+  }
   int rc;
   stage_begin(ST_ROUTE);
   if ((rc = launched(launch_tree_rows(a, ns, g_stream), "router + shared gate / up"))) return rc;
@@ -362,7 +377,7 @@ static int side_get(Side** out) {
 
 // the grouped-GEMM tier: exact routing, the dispatch permutation, expert GEMMs on MFMA, combine
 static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const float* x1, float* y, uint32_t* ids,
-                        float* wt, uint8_t* sc, const ExactScratch& s) {
+                        float* wt, uint8_t* sc, const ExactScratch& s, const NormIn* nin) {
   const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
   if (fg != fu) return fail(LLB_HIP_EINVAL, "f16 tier: gate and up in one format");
   if (L->sf && L->fsg != L->fsu) return fail(LLB_HIP_EINVAL, "f16 tier: shared gate and up in one format");
@@ -371,7 +386,7 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
   const GemmScratch gs = gemm_layout(L, T);
   uint8_t* gb = sc + s.total;
   int rc;
-  if ((rc = route(L, T, h2, ids, wt, sc, s, false))) return rc;
+  if ((rc = route(L, T, h2, ids, wt, sc, s, false, nullptr, nin))) return rc;
   const uint32_t n = T * L->nk;
   uint32_t* off = (uint32_t*)(gb + gs.off);
   uint32_t* xmap = (uint32_t*)(gb + gs.xmap);
@@ -546,8 +561,34 @@ int llb_moe_hip_status(llb_dptr scratch, const llb_moe_layer* L, uint32_t T) {
   return 0;
 }
 
+static int forward_impl(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dptr x1, llb_dptr y, llb_dptr ids,
+                        llb_dptr wt, llb_dptr scratch, size_t scratch_bytes, int tier, const NormIn* nin);
+
 int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dptr x1, llb_dptr y, llb_dptr ids,
                         llb_dptr wt, llb_dptr scratch, size_t scratch_bytes, int tier) {
+  return forward_impl(L, T, h2, x1, y, ids, wt, scratch, scratch_bytes, tier, nullptr);
+}
+
+int llb_moe_hip_forward_norm(const llb_moe_layer* L, uint32_t T, llb_dptr x, llb_dptr z, llb_dptr w, float eps,
+                             llb_dptr x1, llb_dptr h2, llb_dptr y, llb_dptr ids, llb_dptr wt, llb_dptr scratch,
+                             size_t scratch_bytes, int tier) {
+  if (!L) return fail(LLB_HIP_EINVAL, "null layer");
+  if (!x || !z || !w || !x1 || !h2) return fail(LLB_HIP_EINVAL, "forward_norm: null input-step buffer");
+  if (T == 0) return 0;
+  // the router launch carries the input step for T < 16 (its one-token-a-block kernel), outside the
+  // fused persistent path; otherwise llb_rmsnorm_add's own launch first -- the same bits either way
+  const bool ride = T < 16 && L->dm % 4 == 0 && L->dm <= 16384 &&
+                    !(tier == LLB_MOE_EXACT && g_fused && T <= 8);
+  if (!ride) {
+    int rc = llb_moe_hip_rmsnorm_add(x, z, w, eps, T, L->dm, x1, h2);
+    return rc ? rc : llb_moe_hip_forward(L, T, h2, x1, y, ids, wt, scratch, scratch_bytes, tier);
+  }
+  const NormIn nin{dp<float>(x), dp<float>(z), dp<float>(w), eps, dp<float>(x1), dp<float>(h2)};
+  return forward_impl(L, T, h2, x1, y, ids, wt, scratch, scratch_bytes, tier, &nin);
+}
+
+static int forward_impl(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dptr x1, llb_dptr y, llb_dptr ids,
+                        llb_dptr wt, llb_dptr scratch, size_t scratch_bytes, int tier, const NormIn* nin) {
   int rc = check_layer(L, tier);
   if (rc) return rc;
   if (T == 0) return 0;
@@ -562,7 +603,7 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
   if (tier == LLB_MOE_EXACT && g_fused && T <= 8 && fg == fu && fused_supported(fg, fd, fs, nsp))
     return fused_forward(L, T, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt), sc, s);
   if (tier == LLB_MOE_F16)
-    return gemm_forward(L, T, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt), sc, s);
+    return gemm_forward(L, T, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt), sc, s, nin);
   // one token: the exact tier routes inside its gate / up launch (one launch fewer a layer; every
   // block recomputes the token's routing, which only pays off for a single token)
   // stream residency (the k chosen experts copied in per token): exact tier, one token, eager
@@ -573,7 +614,7 @@ int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
   const bool fuse_topk = (tier == LLB_MOE_Q8 || fg == fu) && T == 1 && !streamed;
   // the q8 tier computes the shared gate / up rows in its own gate / up launch (int8 dots)
   if ((rc = route(L, T, dp<float>(h2), dp<uint32_t>(ids), dp<float>(wt), sc, s, tier != LLB_MOE_Q8,
-                  fuse_topk ? &tk : nullptr)))
+                  fuse_topk ? &tk : nullptr, nin)))
     return rc;
   const uint64_t rbg = row_bytes(fg, L->dm), rbu = row_bytes(fu, L->dm);
   const uint64_t esg = (uint64_t)(fz ? 2 : 1) * L->ef * rbg;

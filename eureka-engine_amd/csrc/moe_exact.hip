@@ -81,8 +81,44 @@ DEV void tree_body(const TreeArgs& a, u32 bx, u32 t, u32 L, float* xsh) {
   const u32 nl4 = a.cols / 4;
   const float4* x4 = (const float4*)(a.x + (u64)t * a.xstride);
   float4 xc[NQ];
+  if (a.nz) {
+    // llb_rmsnorm_add's arithmetic (k_rmsnorm_add) on this layout: x1 = x + z; the squares' sum is the
+    // balanced pairwise tree in column order over 64 NQ float4 groups (2^cdepth leaves, +0 pads) -- in
+    // the group, then six levels across lanes (group 64 q + L), then over q in the lane -- the same
+    // tree k_rmsnorm_add sums; s = 1 / sqrt(sum / cols + eps), h2 = (x1 s) w
+    const float4* z4 = (const float4*)(a.nz + (u64)t * a.xstride);
+    const float4* w4 = (const float4*)a.nw;
+    float4 v[NQ], wv[NQ];
 #pragma unroll
-  for (u32 q = 0; q < NQ; q++) xc[q] = 64 * q + L < nl4 ? x4[64 * q + L] : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (u32 q = 0; q < NQ; q++) {
+      const bool in = 64 * q + L < nl4;
+      const float4 xa = in ? x4[64 * q + L] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 za = in ? z4[64 * q + L] : make_float4(0.f, 0.f, 0.f, 0.f);
+      wv[q] = in ? w4[64 * q + L] : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[q] = make_float4(xa.x + za.x, xa.y + za.y, xa.z + za.z, xa.w + za.w);
+    }
+    float n[NQ];
+#pragma unroll
+    for (u32 q = 0; q < NQ; q++)
+      n[q] = tree64_asc((v[q].x * v[q].x + v[q].y * v[q].y) + (v[q].z * v[q].z + v[q].w * v[q].w));
+    const float sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, tree_in_lane<NQ>(n))));
+    const float s = 1.0f / __builtin_sqrtf(sum / (float)a.cols + a.eps);  // correctly rounded, as k_rmsnorm_add
+#pragma unroll
+    for (u32 q = 0; q < NQ; q++)
+      xc[q] = make_float4((v[q].x * s) * wv[q].x, (v[q].y * s) * wv[q].y, (v[q].z * s) * wv[q].z, (v[q].w * s) * wv[q].w);
+    if (bx == 0) {
+#pragma unroll
+      for (u32 q = 0; q < NQ; q++) {
+        if (64 * q + L < nl4) {
+          ((float4*)(a.x1o + (u64)t * a.xstride))[64 * q + L] = v[q];
+          ((float4*)(a.h2o + (u64)t * a.xstride))[64 * q + L] = xc[q];
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (u32 q = 0; q < NQ; q++) xc[q] = 64 * q + L < nl4 ? x4[64 * q + L] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   u32 row[RPW], sgi[RPW];
 #pragma unroll
   for (u32 k = 0; k < RPW; k++) {
@@ -1186,6 +1222,7 @@ int launch_tree_rows(const TreeArgs& a, u32 nsp, hipStream_t st) {
   u32 rows = 0;
   for (u32 i = 0; i < a.nseg; i++) rows += a.seg[i].rows;
   if (rows == 0) return 0;
+  if (a.nz && (a.T >= 16 || a.cols % 4)) return -1;  // the input step rides on the one-token-a-block kernel only
   if (a.T >= 16 && nsp <= 2) {  // token tiles: weights read once a tile
     const u32 tt = 4, nt = (a.T + tt - 1) / tt, slots = 2 * cu_count();
     const size_t sm = (size_t)tt * 64 * (32 * nsp + 4) * 4;

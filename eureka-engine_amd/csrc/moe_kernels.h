@@ -34,6 +34,13 @@ struct TreeArgs {
   uint32_t cols;
   const float* x;  // [T][xstride]
   uint32_t T, xstride, tch;
+  // the input step inside (T < 16; nz set): x is the pre-norm input, x1 = x + nz, h2 = (x1 s) nw with
+  // s = 1 / sqrt(sum x1^2 / cols + eps); blocks of row block 0 store x1o / h2o for the later stages
+  const float* nz;
+  const float* nw;
+  float eps;
+  float* x1o;
+  float* h2o;
 };
 struct TopkArgs {
   const float* lg;  // [T][lstride]: ne logits, then the shared gate's when has_sg

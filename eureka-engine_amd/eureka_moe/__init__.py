@@ -69,6 +69,9 @@ _SIGS = {
     "llb_moe_hip_scratch_bytes": (C.c_size_t, [C.POINTER(MoeLayer), C.c_uint32, C.c_int]),
     "llb_moe_hip_forward": (C.c_int, [C.POINTER(MoeLayer), C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64,
                                       C.c_uint64, C.c_uint64, C.c_size_t, C.c_int]),
+    "llb_moe_hip_forward_norm": (C.c_int, [C.POINTER(MoeLayer), C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64,
+                                           C.c_float, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64,
+                                           C.c_uint64, C.c_size_t, C.c_int]),
     "llb_moe_hip_set_fused": (C.c_int, [C.c_int]),
     "llb_moe_hip_pack_bytes": (C.c_size_t, [C.POINTER(MoeLayer)]),
     "llb_gguf_open": (C.c_void_p, [C.c_char_p]),

@@ -112,6 +112,16 @@ size_t llb_moe_hip_scratch_bytes(const llb_moe_layer* L, uint32_t T, int tier);
 int llb_moe_hip_forward(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dptr x1, llb_dptr y, llb_dptr ids,
                         llb_dptr wt, llb_dptr scratch, size_t scratch_bytes, int tier);
 
+/* One layer with its input step: x1 = x + z and h2 = rmsnorm(x1) w, as llb_moe_hip_rmsnorm_add computes
+ * them (llb_rmsnorm_add, tools/payload-fuse.patch:106-127), then llb_moe_hip_forward(L, T, h2, x1, ...).
+ * x1 and h2 ([T][dm]) are written too. For T < 16 the router launch computes the input step itself
+ * (each of its blocks recomputes the token's norm), one launch fewer a layer; otherwise the input step
+ * runs as its own launch first. The bits are the two calls' either way. No single counterpart in the
+ * reference: there llb_rmsnorm_add and llb_moe_run are separate launches (host/llb_host.c:622-724). */
+int llb_moe_hip_forward_norm(const llb_moe_layer* L, uint32_t T, llb_dptr x, llb_dptr z, llb_dptr w, float eps,
+                             llb_dptr x1, llb_dptr h2, llb_dptr y, llb_dptr ids, llb_dptr wt, llb_dptr scratch,
+                             size_t scratch_bytes, int tier);
+
 /* The exact tier at T <= 8 runs a layer as one persistent launch (the "fused" path; the four-launch
  * sequence otherwise). The fused path keeps 6 counters in the scratch, which must be zero before
  * its first use (llb_hip_alloc_zero gives that) and which every launch leaves zero. on = 0 forces

@@ -322,6 +322,36 @@ def test_graph_replays_match_eager(dev, name, T, tier):
         other.free()
 
 
+@pytest.mark.parametrize("name,T,tier", [("c2", 1, em.EXACT), ("c2", 5, em.EXACT), ("c2", 1, em.Q8), ("c1", 4, em.Q8),
+                                         ("c2", 8, em.F16), ("c1", 20, em.EXACT)])
+def test_forward_norm_matches_two_calls(dev, name, T, tier):
+    """llb_moe_hip_forward_norm (the input step inside the router launch for T < 16, its own launch
+    from 16 on) gives the bits of llb_moe_hip_rmsnorm_add followed by llb_moe_hip_forward: x1, h2, y,
+    ids and wt"""
+    shape = em.SHAPES[name]
+    _say("forward_norm", name, "T", T, "tier", tier)
+    layer = em.Layer(dev, shape, seed=12)
+    run = em.Runner(dev, shape, T, tier=tier)
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((T, shape.dm)).astype(np.float32)
+    z = rng.standard_normal((T, shape.dm)).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(shape.dm)).astype(np.float32)
+    px, pz, pw = dev.upload(x), dev.upload(z), dev.upload(w)
+    x1b, h2b = dev.alloc(x.nbytes), dev.alloc(x.nbytes)
+    lib = dev.lib
+    dev.check(lib.llb_moe_hip_rmsnorm_add(px, pz, pw, 1e-6, T, shape.dm, run.x1, run.h2))
+    dev.check(lib.llb_moe_hip_forward(C.byref(layer.desc), T, run.h2, run.x1, run.y, run.ids, run.wt, run.scratch,
+                                      run.scratch_bytes, tier))
+    ref = run.outputs() + (dev.read(run.x1, x.shape, np.float32), dev.read(run.h2, x.shape, np.float32))
+    dev.check(lib.llb_moe_hip_forward_norm(C.byref(layer.desc), T, px, pz, pw, 1e-6, x1b, h2b, run.y, run.ids,
+                                           run.wt, run.scratch, run.scratch_bytes, tier))
+    got = run.outputs() + (dev.read(x1b, x.shape, np.float32), dev.read(h2b, x.shape, np.float32))
+    run.free()
+    layer.free()
+    for nm, a, b in zip(("y", "ids", "wt", "x1", "h2"), got, ref):
+        assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32)), nm
+
+
 def _nan_equal(a, b):
     a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
     ok = (np.isnan(a) & np.isnan(b)) | (a.view(np.uint32) == b.view(np.uint32))
