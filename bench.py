@@ -180,13 +180,16 @@ def batched(dev, shape, T, layers, steps, warmup, tier):
     dev.timing(False)
     ids = dev.read(run.ids, (T, shape.nk), np.uint32)
     uniq = int(np.unique(ids).size)
+    hist = np.bincount(ids.ravel(), minlength=shape.ne)
+    load = {"tokens_per_expert_top10": sorted(hist.tolist(), reverse=True)[:10], "experts_hit": uniq,
+            "experts_with_20_or_more": int((hist >= 20).sum()), "experts_unused": int((hist == 0).sum())}
     run.free()
     for L in Ls:
         L.free()
     us = wall / (steps * layers) * 1e6
     byts = uniq * shape.expert_bytes() + shape.ne * shape.dm * 4 + shape.shared_bytes()
     return {"us_per_layer": round(us, 2), "us_per_token_layer": round(us / T, 3), "T": T,
-            "unique_experts_last_layer": uniq, "algorithmic_bytes_last_layer": byts,
+            "unique_experts_last_layer": uniq, "expert_load_last_layer": load, "algorithmic_bytes_last_layer": byts,
             "stages_us": {k: round(v[0], 2) for k, v in st.items()},
             "hbm_frac_last_layer": round(byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
