@@ -349,67 +349,6 @@ DEV void wave_amax(float& bv, u32& bi) {
 // argmax (ties to the lower index) would take e, so the experts with rank < k are the top k in that
 // order -- independent compares, no serial chain. wt_j = p / max(sum of the k p in rank order,
 // 2^-14); sgo = sigmoid(sg). Thread t holds experts t, t + 256, t + 512, t + 768.
-// the value of lane L ^ J (J a power of two below 64), through DPP / permlane swaps
-template <u32 J> DEV u32 lane_xor(u32 v, u32 L) {
-  if constexpr (J == 1) return dppu<DPP_XOR1>(v);
-  else if constexpr (J == 2) return dppu<DPP_XOR2>(v);
-  else if constexpr (J == 4) {
-    // no select (a select around DPP may become a branch, and DPP reads of lanes switched off by it
-    // return the old operand): banks 0 and 2 of each row (lanes with bit 2 clear) take lane + 4
-    // (row_ror:12), then banks 1 and 3 take lane - 4 (row_ror:4) over that result
-    const u32 up = (u32)__builtin_amdgcn_update_dpp(0, (int)v, DPP_UP4, 0xf, 0x5, false);
-    return (u32)__builtin_amdgcn_update_dpp((int)up, (int)v, 0x124, 0xf, 0xa, false);
-  }
-  else if constexpr (J == 8) return dppu<DPP_XOR8>(v);
-  else if constexpr (J == 16) {
-    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-    return (L & 16) ? r[0] : r[1];
-  } else {
-    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    return (L & 32) ? r[0] : r[1];
-  }
-}
-// one compare-exchange stage of a bitonic sort over the wave's 64 keys: lane L keeps the larger of
-// its key and lane L ^ J's when (L & J) == 0 matches the block's direction (descending where
-// (L & K) == 0), else the smaller
-template <u32 K, u32 J> DEV u64 bitonic_step(u64 key, u32 L) {
-  const u32 hi = lane_xor<J>((u32)(key >> 32), L), lo = lane_xor<J>((u32)key, L);
-  const u64 other = (u64)hi << 32 | lo;
-  const bool keep_max = ((L & J) == 0) == ((L & K) == 0);
-  const bool gt = other > key;
-  return gt == keep_max ? other : key;
-}
-// 32-bit values: the same network with max / min (no index, for when only values matter)
-template <u32 K, u32 J> DEV u32 bitonic_step32(u32 v, u32 L) {
-  const u32 o = lane_xor<J>(v, L);
-  return (((L & J) == 0) == ((L & K) == 0)) ? max(v, o) : min(v, o);
-}
-DEV u32 wave_sort_desc32(u32 k, u32 L) {
-  k = bitonic_step32<2, 1>(k, L);
-  k = bitonic_step32<4, 2>(k, L);   k = bitonic_step32<4, 1>(k, L);
-  k = bitonic_step32<8, 4>(k, L);   k = bitonic_step32<8, 2>(k, L);   k = bitonic_step32<8, 1>(k, L);
-  k = bitonic_step32<16, 8>(k, L);  k = bitonic_step32<16, 4>(k, L);  k = bitonic_step32<16, 2>(k, L);
-  k = bitonic_step32<16, 1>(k, L);
-  k = bitonic_step32<32, 16>(k, L); k = bitonic_step32<32, 8>(k, L);  k = bitonic_step32<32, 4>(k, L);
-  k = bitonic_step32<32, 2>(k, L);  k = bitonic_step32<32, 1>(k, L);
-  k = bitonic_step32<64, 32>(k, L); k = bitonic_step32<64, 16>(k, L); k = bitonic_step32<64, 8>(k, L);
-  k = bitonic_step32<64, 4>(k, L);  k = bitonic_step32<64, 2>(k, L);  k = bitonic_step32<64, 1>(k, L);
-  return k;
-}
-// the wave's 64 keys sorted descending: lane i holds the i-th largest
-DEV u64 wave_sort_desc(u64 k, u32 L) {
-  k = bitonic_step<2, 1>(k, L);
-  k = bitonic_step<4, 2>(k, L);   k = bitonic_step<4, 1>(k, L);
-  k = bitonic_step<8, 4>(k, L);   k = bitonic_step<8, 2>(k, L);   k = bitonic_step<8, 1>(k, L);
-  k = bitonic_step<16, 8>(k, L);  k = bitonic_step<16, 4>(k, L);  k = bitonic_step<16, 2>(k, L);
-  k = bitonic_step<16, 1>(k, L);
-  k = bitonic_step<32, 16>(k, L); k = bitonic_step<32, 8>(k, L);  k = bitonic_step<32, 4>(k, L);
-  k = bitonic_step<32, 2>(k, L);  k = bitonic_step<32, 1>(k, L);
-  k = bitonic_step<64, 32>(k, L); k = bitonic_step<64, 16>(k, L); k = bitonic_step<64, 8>(k, L);
-  k = bitonic_step<64, 4>(k, L);  k = bitonic_step<64, 2>(k, L);  k = bitonic_step<64, 1>(k, L);
-  return k;
-}
-
 // a token's routing out of topk_body256's LDS into ids / wt / sgo (the renormalised weights as
 // llb_moe_topk: the rank-order sum of the chosen p, clamped at 2^-14, divides each)
 DEV void topk_write(const TopkArgs& a, u32 t, const float* sm) {
@@ -489,8 +428,8 @@ DEV void topk_body256(const TopkArgs& a, u32 t, float* sm, bool wr) {
   float* lm = red + 64;                // [64] lane maxima
   if (w == 0) {
     // Order keys: (bits of p) << 32 | ~e. p >= 0, so its bits order like p; a larger key is a larger
-    // p, then a lower index. -inf (and NaN) map to key 0, below every real p. The 64 lane maxima and
-    // then the (at most 64) candidates are ranked by a bitonic sort across the wave.
+    // p, then a lower index. -inf (and NaN) map to key 0, below every real p. tau comes from the 64
+    // lane maxima by a radix select over their bits; the (at most 64) candidates are ranked by counting.
     u64* kk = (u64*)cv;  // [64] candidate keys
     if (L < a.nk) ids[L] = 0;  // a valid expert whatever happens below (NaN logits rank nothing)
     const u32 nj = (a.ne + 63) / 64;
@@ -501,12 +440,19 @@ DEV void topk_body256(const TopkArgs& a, u32 t, float* sm, bool wr) {
 #pragma unroll
     for (u32 j = 1; j < 16; j++)
       if (j < nj) m = fmaxf(m, pv[j]);
-    // tau needs only the value of the nk-th largest lane maximum: sort the bits (p >= 0 orders
-    // like its bits; -inf lanes as 0)
+    // tau only has to be a lower bound of the nk-th largest p that leaves few candidates: the largest t
+    // on a grid of 2^16 (sign, exponent and the top 7 mantissa bits of p >= 0, whose bits order like
+    // its value) with at least nk lane maxima >= t -- so at least nk experts have p >= t -- by a
+    // bitwise radix select over the maxima's top 16 bits (-inf and NaN lanes as 0)
     const u32 mb = (L < a.ne && m >= 0.0f) ? __float_as_uint(m) : 0u;
     PHASE(40);
-    const u32 sb = wave_sort_desc32(mb, L);
-    const float tau = __uint_as_float((u32)__builtin_amdgcn_readlane((int)sb, (int)(a.nk - 1)));
+    u32 tb = 0;
+#pragma unroll
+    for (int bit = 31; bit >= 16; bit--) {
+      const u32 c = tb | (1u << bit);
+      if ((u32)__popcll(__ballot(mb >= c)) >= a.nk) tb = c;
+    }
+    const float tau = __uint_as_float(tb);
     kk[L] = 0ull;
     WAVE_SYNC();
     PHASE(41);
@@ -524,10 +470,19 @@ DEV void topk_body256(const TopkArgs& a, u32 t, float* sm, bool wr) {
     WAVE_SYNC();
     PHASE(42);
     if (base <= 64) {
-      const u64 ck = wave_sort_desc(kk[L], L);  // zero keys (no candidate) sort last
-      if (L < a.nk && ck != 0ull) {  // a zero key is no candidate: the slot keeps expert 0
-        ids[L] = 0xFFFFFFFFu - (u32)ck;
-        wv[L] = __uint_as_float((u32)(ck >> 32));
+      // a candidate's rank is the number of larger keys among the candidates (keys are distinct: the
+      // index is in the low word), read as LDS broadcasts; ranks below nk are the top k in order
+      const u64 mine = kk[L];
+      const u32 mhi = (u32)(mine >> 32), mlo = (u32)mine;
+      u32 rk = 0;
+      for (u32 j = 0; j < base; j++) {  // lane j's key, read across the wave (no LDS round trip)
+        const u64 o = (u64)(u32)__builtin_amdgcn_readlane((int)mhi, (int)j) << 32 |
+                      (u32)__builtin_amdgcn_readlane((int)mlo, (int)j);
+        rk += o > mine ? 1u : 0u;
+      }
+      if (L < base && rk < a.nk) {  // fewer than nk candidates (NaN logits): the other slots keep expert 0
+        ids[rk] = 0xFFFFFFFFu - (u32)mine;
+        wv[rk] = __uint_as_float((u32)(mine >> 32));
       }
     }
     PHASE(43);
