@@ -3,6 +3,8 @@ import ctypes as C
 import os
 import re
 
+import pytest
+
 import eureka_moe as em
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -37,3 +39,48 @@ def test_load_raises_without_library(tmp_path):
         assert "no fallback" in str(e)
     else:
         raise AssertionError("load() must fail loudly")
+
+
+# ---- the layer entry points refuse what they cannot run, before any device call, and name the rule
+DUMMY = 0x10000  # a nonzero address that the checks below never reach
+
+
+def _layer(**kw):
+    s = em.SHAPES["c2"]
+    d = dict(dm=s.dm, ne=s.ne, nk=s.nk, ef=s.ef, sf=s.sf, fx=s.fx, fsg=s.fsg, fsu=s.fsu, fsd=s.fsd, pad=0,
+             router=DUMMY, shgate=DUMMY, G=DUMMY, U=DUMMY, D=DUMMY, SG=DUMMY, SU=DUMMY, SD=DUMMY)
+    d.update(kw)
+    L = em.MoeLayer()
+    for k, v in d.items():
+        setattr(L, k, v)
+    return L
+
+
+def _forward(lib, L, T=1, sb=1 << 30, tier=em.EXACT, bufs=DUMMY):
+    return lib.llb_moe_hip_forward(C.byref(L), T, bufs, 0, bufs, bufs, bufs, bufs, sb, tier)
+
+
+@pytest.mark.parametrize("change,rule", [
+    (dict(dm=2000), "multiples of 256"), (dict(ef=300), "multiples of 256"), (dict(nk=64), "nk"),
+    (dict(nk=0), "nk"), (dict(ne=2048), "ne <= 1024"), (dict(fx=em.SHAPES["c2"].fx & ~15 | 7), "expert formats"),
+    (dict(router=0), "null weights"), (dict(D=0), "null weights"), (dict(dm=16384), "router"),
+    (dict(sf=300), "shared expert"), (dict(SD=0), "shared expert"), (dict(fsg=em.Q8_0, fsu=em.Q8_0), "shared gate/up"),
+])
+def test_forward_refuses_each_rule(change, rule):
+    lib = em.load()
+    rc = _forward(lib, _layer(**change))
+    assert rc == -1 and rule in lib.llb_hip_last_error().decode(), (rc, lib.llb_hip_last_error())
+
+
+def test_forward_refuses_buffers_tier_and_scratch():
+    lib = em.load()
+    L = _layer()
+    assert _forward(lib, L, bufs=0) == -1 and b"null buffer" in lib.llb_hip_last_error()
+    assert _forward(lib, L, tier=7) == -1 and b"tier" in lib.llb_hip_last_error()
+    need = lib.llb_moe_hip_scratch_bytes(C.byref(L), 1, em.EXACT)
+    assert need > 0
+    assert _forward(lib, L, sb=need - 1) == -3 and b"scratch" in lib.llb_hip_last_error()
+    assert _forward(lib, L, T=0) == 0  # nothing to do: no device call
+    rc = lib.llb_moe_hip_forward_norm(C.byref(L), 1, DUMMY, 0, DUMMY, 1e-6, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY,
+                                      1 << 30, em.EXACT)
+    assert rc == -1 and b"input-step" in lib.llb_hip_last_error()
