@@ -803,6 +803,11 @@ int llb_moe_hip_q8_1(llb_dptr x, uint32_t n, llb_dptr q, llb_dptr ds) {
   return launched(launch_q8_1(dp<float>(x), n, dp<int8_t>(q), dp<float2>(ds), g_stream), "q8_1");
 }
 
+int llb_moe_hip_exp(llb_dptr x, uint64_t n, llb_dptr y) {
+  if (n && (!x || !y)) return fail(LLB_HIP_EINVAL, "exp: null buffer");
+  return launched(launch_exp(dp<float>(x), dp<float>(y), n, g_stream), "exp");
+}
+
 int llb_moe_hip_dequant(uint32_t fm, llb_dptr W, uint32_t rows, uint32_t cols, llb_dptr out) {
   if (!row_bytes(fm, cols) || cols % 32 || (fm != LLB_FM_F32 && fm != LLB_FM_Q8_0 && cols % 256))
     return fail(LLB_HIP_EINVAL, "dequant: bad format / width");

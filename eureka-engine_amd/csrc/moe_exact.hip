@@ -1336,6 +1336,18 @@ bool fused_supported(u32 fg, u32 fd, u32 fs, u32 nsp) {
   return false;
 }
 
+// the path's exp (the float of the double exp, as every softmax, SwiGLU and sigmoid here uses it)
+__global__ void __launch_bounds__(256) k_exp_f(const float* __restrict__ x, float* __restrict__ y, u64 n) {
+  const u64 i = (u64)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) y[i] = exp_f(x[i]);
+}
+int launch_exp(const float* x, float* y, u64 n, hipStream_t st) {
+  if (n == 0) return 0;
+  if ((n + 255) / 256 > 0x7fffffffull) return -1;
+  hipLaunchKernelGGL(k_exp_f, dim3((u32)((n + 255) / 256)), dim3(256), 0, st, x, y, n);
+  return 0;
+}
+
 int launch_dequant(u32 fm, const u8* W, u64 rb, u32 rows, u32 cols, float* out, hipStream_t st) {
   const u64 n = (u64)rows * (cols / 32);
   dim3 grid((u32)((n + 255) / 256));

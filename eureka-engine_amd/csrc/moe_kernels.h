@@ -145,5 +145,6 @@ int launch_pack(uint32_t fm, const uint8_t* W, uint64_t es, uint64_t rb, uint32_
                 uint8_t* P, hipStream_t st);
 int launch_combine(const float* out, const uint32_t* inv, const float* wt, uint32_t nk, const float* shd,
                    const float* sgo, const float* x1, float* y, uint32_t dm, uint32_t T, hipStream_t st);
+int launch_exp(const float* x, float* y, uint64_t n, hipStream_t st);
 int launch_dequant(uint32_t fm, const uint8_t* W, uint64_t rb, uint32_t rows, uint32_t cols, float* out,
                    hipStream_t st);

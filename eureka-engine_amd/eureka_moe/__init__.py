@@ -93,6 +93,7 @@ _SIGS = {
     "llb_moe_hip_rmsnorm_add": (C.c_int, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_float, C.c_uint32, C.c_uint32,
                                           C.c_uint64, C.c_uint64]),
     "llb_moe_hip_dequant": (C.c_int, [C.c_uint32, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint64]),
+    "llb_moe_hip_exp": (C.c_int, [C.c_uint64, C.c_uint64, C.c_uint64]),
     "llb_moe_hip_timing": (C.c_int, [C.c_int]),
     "llb_hip_spin": (C.c_int, [C.c_uint32]),
     "llb_moe_hip_timing_read": (C.c_int, [C.POINTER(C.c_double), C.POINTER(C.c_long), C.c_int]),

@@ -181,6 +181,9 @@ int llb_moe_hip_group(llb_dptr ids, uint32_t n, uint32_t nk, uint32_t ne, llb_dp
 int llb_moe_hip_q8_1(llb_dptr x, uint32_t n, llb_dptr q, llb_dptr ds);
 /* rows of a stack dequantized to f32 (the decoders the kernels use; q8g_w / q4k_w / q6k_w / q5k_w) */
 int llb_moe_hip_dequant(uint32_t fm, llb_dptr W, uint32_t rows, uint32_t cols, llb_dptr out);
+/* y[i] = (float)exp((double)x[i]), the exp every softmax, SwiGLU and sigmoid of the path uses (attn_exp,
+ * tools/payload-attn.patch:57-59; hf_exp, tools/qwen35_engine.c:46-50): for parity checks */
+int llb_moe_hip_exp(llb_dptr x, uint64_t n, llb_dptr y);
 
 /* ---- per-stage timing (no counterpart in the reference; its LLB_STEP_US times whole steps,
  * host/llb_host.c:2873-2891): on = 1 resets and starts a tally of HIP-event intervals around each

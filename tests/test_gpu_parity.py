@@ -352,6 +352,32 @@ def test_forward_norm_matches_two_calls(dev, name, T, tier):
         assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32)), nm
 
 
+def test_exp_matches_the_host_double_exp(dev):
+    """the device's float(exp(double)) against the host's on 2^22 arguments covering the softmax's
+    range (l - max in [-104, 0], dense near 0), SwiGLU / sigmoid arguments in [-40, 40], the subnormal and
+    overflow edges and the special values; bit for bit (numpy's float64 exp on all of them, glibc's
+    through the oracle on a sample, and the reference CPU twin's hf_exp through oracle/_ref where built)"""
+    rng = np.random.default_rng(17)
+    x = np.concatenate([
+        -rng.exponential(3.0, 1 << 20), rng.uniform(-104.0, 0.0, 1 << 20), rng.uniform(-40.0, 40.0, 1 << 20),
+        rng.standard_normal(1 << 20) * 4.0,
+        np.array([0.0, -0.0, 88.72, 88.73, 89.0, -87.33, -103.27, -103.28, -104.0, -150.0, 1e-30, -1e-30,
+                  np.inf, -np.inf, np.nan], np.float64)]).astype(np.float32)
+    px, py = dev.upload(x), dev.alloc(x.nbytes)
+    dev.check(dev.lib.llb_moe_hip_exp(px, x.size, py))
+    got = dev.read(py, x.shape, np.float32)
+    with np.errstate(over="ignore", under="ignore"):
+        ref = np.exp(x.astype(np.float64)).astype(np.float32)
+    assert _nan_equal(got, ref)
+    idx = rng.choice(x.size, 20000, replace=False)
+    for i in idx:
+        assert got[i].view(np.uint32) == np.float32(ol.lib().mo_exp(float(x[i]))).view(np.uint32), x[i]
+    ref_lib = ol.ref_lib()
+    if ref_lib is not None:
+        for i in idx[:5000]:
+            assert got[i].view(np.uint32) == np.float32(ref_lib.ref_hf_exp(float(x[i]))).view(np.uint32), x[i]
+
+
 def _nan_equal(a, b):
     a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
     ok = (np.isnan(a) & np.isnan(b)) | (a.view(np.uint32) == b.view(np.uint32))
