@@ -273,7 +273,7 @@ static GemmScratch gemm_layout(const llb_moe_layer* L, uint32_t T) {
   g.xmap = o; o += al(n * 4);
   g.inv = o; o += al(n * 4);
   g.act = o; o += al(n * L->ef * 2);
-  g.out = o; o += al(n * L->dm * 4);
+  g.out = o; o += al(n * L->dm * 2);
   g.sact = o; o += al((size_t)T * L->sf * 2 + 4);
   g.shd = o; o += al((size_t)T * L->dm * 4);
   g.total = o;
@@ -469,6 +469,7 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
   d.arows = n;
   d.xmap = nullptr;
   d.out = gb + gs.out;
+  d.o16 = 1;
   d.P0 = L->PD ? dp<uint8_t>(L->PD) : nullptr;
   d.P1 = nullptr;
   d.pes = pack_bytes(fd, L->dm, L->ef);
@@ -476,7 +477,7 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
   if ((rc = launched(launch_moe_gemm(d, fd, 1, maxt, g_stream), "expert down GEMM"))) return rc;
   stage_end(ST_DN);
   if (side && (rc = hip_ok(hipStreamWaitEvent(g_stream, side->join, 0), "join hipStreamWaitEvent"))) return rc;
-  return launched(launch_combine((const float*)(gb + gs.out), inv, wt, L->nk, shd, (const float*)(sc + s.sgo), x1, y,
+  return launched(launch_combine((const _Float16*)(gb + gs.out), inv, wt, L->nk, shd, (const float*)(sc + s.sgo), x1, y,
                                  L->dm, T, g_stream),
                   "combine");
 }
