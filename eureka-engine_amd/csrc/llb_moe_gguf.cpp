@@ -17,10 +17,13 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <condition_variable>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/llb_moe_hip.h"
@@ -430,9 +433,78 @@ int llb_moe_hip_load_layer(llb_gguf* g, uint32_t layer, int mode, llb_moe_layer*
 
 }  // extern "C"
 
+// The stream gather's worker pool (the reference spreads the per-token copy over 8 threads,
+// host/llb_host.c:680-696). One process-wide pool, made on the first streamed token and never torn down:
+// its threads sleep on the condition variable between tokens, and at exit the process ends them. The
+// calling thread is worker 0. A job is a list of source segments laid end to end in dst; the bytes
+// [0, total) are cut into kGather equal pieces, piece i copied by worker i. run() returns when every
+// piece is copied, and the mutex orders those writes before the caller's upload.
+namespace {
+constexpr unsigned kGather = 8;
+struct Seg {
+  const uint8_t* src;
+  uint64_t len;
+};
+struct GatherPool {
+  std::mutex call;  // one job at a time: callers on several threads queue here
+  std::mutex m;
+  std::condition_variable go, done;
+  uint64_t gen = 0;
+  unsigned left = 0;
+  const Seg* seg = nullptr;
+  size_t nseg = 0;
+  uint64_t total = 0;
+  uint8_t* dst = nullptr;
+  void piece(unsigned i) {
+    const uint64_t lo = total * i / kGather, hi = total * (i + 1) / kGather;
+    uint64_t base = 0;
+    for (size_t k = 0; k < nseg && base < hi; base += seg[k++].len) {
+      const uint64_t a = lo > base ? lo : base, b = hi < base + seg[k].len ? hi : base + seg[k].len;
+      if (a < b) memcpy(dst + a, seg[k].src + (a - base), b - a);
+    }
+  }
+  void worker(unsigned i) {
+    uint64_t seen = 0;
+    for (;;) {
+      {
+        std::unique_lock<std::mutex> lk(m);
+        go.wait(lk, [&] { return gen != seen; });
+        seen = gen;
+      }
+      piece(i);
+      std::lock_guard<std::mutex> lk(m);
+      if (--left == 0) done.notify_one();
+    }
+  }
+  void run(uint8_t* d, const std::vector<Seg>& sv) {
+    std::lock_guard<std::mutex> one(call);
+    {
+      std::lock_guard<std::mutex> lk(m);
+      dst = d, seg = sv.data(), nseg = sv.size(), total = 0;
+      for (const Seg& x : sv) total += x.len;
+      left = kGather - 1;
+      gen++;
+    }
+    go.notify_all();
+    piece(0);
+    std::unique_lock<std::mutex> lk(m);
+    done.wait(lk, [&] { return left == 0; });
+  }
+};
+GatherPool* gather_pool() {
+  static std::once_flag once;
+  static GatherPool* p = nullptr;
+  std::call_once(once, [] {
+    p = new GatherPool;  // never freed: detached workers wait on it until the process ends
+    for (unsigned i = 1; i < kGather; i++) std::thread(&GatherPool::worker, p, i).detach();
+  });
+  return p;
+}
+}  // namespace
+
 // the k chosen experts of one token into the device staging (the reference's per-token copy,
-// host/llb_host.c:680-696): ids read back, each expert's gate (+ up) and down bytes gathered from the
-// mapped file into pinned memory, then uploaded in order on the library stream. The slot ids 0..k-1
+// host/llb_host.c:680-696): ids read back, the experts' gate (+ up) and down bytes gathered from the
+// mapped file into pinned memory by the pool, then uploaded on the library stream. The slot ids 0..k-1
 // replace the experts' ids for the expert kernels.
 int stream_stage(const llb_moe_layer* L, const uint32_t* d_ids, const uint32_t** slots) {
   auto* s = (StreamSrc*)(uintptr_t)L->stream;
@@ -442,22 +514,28 @@ int stream_stage(const llb_moe_layer* L, const uint32_t* d_ids, const uint32_t**
   if (hipMemcpyAsync(ids.data(), d_ids, 4ull * s->nk, hipMemcpyDeviceToHost, st) != hipSuccess ||
       hipStreamSynchronize(st) != hipSuccess)
     return llb_fail_msg(LLB_HIP_EDEVICE, "stream: cannot read the chosen experts back");
-  const uint64_t gb = s->esg, ub = s->fused ? 0 : s->esg, db = s->esd, ex = gb + ub + db;
+  const uint64_t gb = s->esg, ub = s->fused ? 0 : s->esg, db = s->esd;
   uint8_t* pin = (uint8_t*)s->pin;
   uint8_t* dev = (uint8_t*)s->dev;
-  for (uint32_t j = 0; j < s->nk; j++) {
-    const uint64_t e = ids[j];
-    if (e >= L->ne) return llb_fail_msg(LLB_HIP_EINVAL, "stream: an expert id out of range");
-    uint8_t* hp = pin + j * ex;
-    memcpy(hp, s->map + s->sg + e * s->esg, gb);
-    if (ub) memcpy(hp + gb, s->map + s->su + e * s->esg, ub);
-    memcpy(hp + gb + ub, s->map + s->sd + e * s->esd, db);
-    // device: gate slots [0, nk gb), up slots [nk gb, nk (gb + ub)), down slots after
-    if (hipMemcpyAsync(dev + j * gb, hp, gb, hipMemcpyHostToDevice, st) != hipSuccess ||
-        (ub && hipMemcpyAsync(dev + s->nk * gb + j * ub, hp + gb, ub, hipMemcpyHostToDevice, st) != hipSuccess) ||
-        hipMemcpyAsync(dev + s->nk * (gb + ub) + j * db, hp + gb + ub, db, hipMemcpyHostToDevice, st) != hipSuccess)
-      return llb_fail_msg(LLB_HIP_EDEVICE, "stream: cannot stage an expert");
-  }
+  for (uint32_t j = 0; j < s->nk; j++)
+    if (ids[j] >= L->ne) return llb_fail_msg(LLB_HIP_EINVAL, "stream: an expert id out of range");
+  // gathered in the device staging's order (the nk gate experts, the nk up experts, the nk down experts)
+  // in two jobs, gate / up then down, each uploaded as one copy: the pool gathers the down experts while
+  // the copy engine uploads gate / up
+  std::vector<Seg> sv;
+  sv.reserve(2 * s->nk);
+  for (uint32_t j = 0; j < s->nk; j++) sv.push_back({s->map + s->sg + ids[j] * s->esg, gb});
+  for (uint32_t j = 0; ub && j < s->nk; j++) sv.push_back({s->map + s->su + ids[j] * s->esg, ub});
+  GatherPool* pool = gather_pool();
+  const uint64_t a = s->nk * (gb + ub);
+  pool->run(pin, sv);
+  if (hipMemcpyAsync(dev, pin, a, hipMemcpyHostToDevice, st) != hipSuccess)
+    return llb_fail_msg(LLB_HIP_EDEVICE, "stream: cannot stage the gate / up experts");
+  sv.clear();
+  for (uint32_t j = 0; j < s->nk; j++) sv.push_back({s->map + s->sd + ids[j] * s->esd, db});
+  pool->run(pin + a, sv);
+  if (hipMemcpyAsync(dev + a, pin + a, s->nk * db, hipMemcpyHostToDevice, st) != hipSuccess)
+    return llb_fail_msg(LLB_HIP_EDEVICE, "stream: cannot stage the down experts");
   *slots = s->slots;
   return 0;
 }
