@@ -434,7 +434,7 @@ int llb_moe_hip_load_layer(llb_gguf* g, uint32_t layer, int mode, llb_moe_layer*
 }  // extern "C"
 
 // The stream gather's worker pool (the reference spreads the per-token copy over 8 threads,
-// host/llb_host.c:680-696). One process-wide pool, made on the first streamed token and never torn down:
+// host/llb_host.c:680-696). One pool a process, made on its first streamed token and never torn down:
 // its threads sleep on the condition variable between tokens, and at exit the process ends them. The
 // calling thread is worker 0. A job is a list of source segments laid end to end in dst; the bytes
 // [0, total) are cut into kGather equal pieces, piece i copied by worker i. run() returns when every
@@ -491,13 +491,18 @@ struct GatherPool {
     done.wait(lk, [&] { return left == 0; });
   }
 };
+// the pool of this process: a child made by fork() inherits the pool's memory but not its threads, so
+// a pool made by another process id is left behind (never touched again) and a new one is made
 GatherPool* gather_pool() {
-  static std::once_flag once;
+  static std::mutex mk;
   static GatherPool* p = nullptr;
-  std::call_once(once, [] {
+  static pid_t owner = 0;
+  std::lock_guard<std::mutex> lk(mk);
+  if (!p || owner != getpid()) {
     p = new GatherPool;  // never freed: detached workers wait on it until the process ends
+    owner = getpid();
     for (unsigned i = 1; i < kGather; i++) std::thread(&GatherPool::worker, p, i).detach();
-  });
+  }
   return p;
 }
 }  // namespace
