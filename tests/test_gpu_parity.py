@@ -616,3 +616,96 @@ def test_gguf_load_same_bits_every_mode(dev, tmp_path, mode):
         ref.free()
         dev.check(dev.lib.llb_moe_hip_unload_layer(C.byref(desc)))
         dev.lib.llb_gguf_close(g)
+
+
+def _fused_desc(dev, ref, s):
+    """the layer `ref` with its gate and up stacks as one fused stack (ffn_gate_up_exps: per expert its ef
+    gate rows, then its ef up rows; fx bit 12, U unused), the same bytes rearranged"""
+    gb, ub, _ = s.stack_bytes()
+    g = dev.read(ref.G, (s.ne, gb // s.ne), np.uint8)
+    u = dev.read(ref.U, (s.ne, ub // s.ne), np.uint8)
+    fused = np.concatenate([g, u], axis=1)
+    pf = dev.upload(fused)
+    desc = em.MoeLayer(s.dm, s.ne, s.nk, s.ef, s.sf, s.fx | 1 << 12, s.fsg, s.fsu, s.fsd, 0, ref.router, ref.shgate,
+                       pf, 0, ref.D, ref.SG, ref.SU, ref.SD, 0)
+    return desc, pf, fused
+
+
+@pytest.mark.parametrize("tier,T,packed", [(em.EXACT, 1, False), (em.EXACT, 5, False), (em.EXACT, 20, False),
+                                           (em.Q8, 1, False), (em.Q8, 4, False), (em.Q8, 12, False),
+                                           (em.F16, 40, False), (em.F16, 40, True)])
+def test_fused_gate_up_stack_same_bits(dev, tier, T, packed):
+    """a fused gate+up stack (the reference's ffn_gate_up_exps layout, fx bit 12) gives the separate
+    stacks' ids, weights and y bits at every tier, GGUF rows and packed tiles alike"""
+    s = SMALL[0]
+    _say("fused gate+up", tier, T, packed)
+    ref = em.Layer(dev, s, seed=5)
+    desc, pf, _ = _fused_desc(dev, ref, s)
+    pk = []
+
+    class Lo:
+        pass
+    lo = Lo()
+    lo.desc = desc
+    try:
+        if packed:
+            ref.pack()
+            n = dev.lib.llb_moe_hip_pack_bytes(C.byref(desc))
+            assert n
+            pk.append(dev.alloc(n))
+            dev.check(dev.lib.llb_moe_hip_pack(C.byref(desc), pk[0], n))
+        run = em.Runner(dev, s, T, tier=tier)
+        for seed in (3, 4):
+            run.gen_inputs(seed)
+            run.forward(ref)
+            y0, i0, w0 = run.outputs()
+            run.forward(lo)
+            y1, i1, w1 = run.outputs()
+            assert np.array_equal(i0, i1) and np.array_equal(w0.view(np.uint32), w1.view(np.uint32))
+            assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32)), np.abs(y0 - y1).max()
+        run.free()
+    finally:
+        for p in pk + [pf]:
+            dev.free(p)
+        ref.free()
+
+
+@pytest.mark.parametrize("mode", [0, 2])
+def test_gguf_fused_gate_up_stack(dev, tmp_path, mode):
+    """a GGUF layer whose gate and up stacks are one blk.N.ffn_gate_up_exps tensor, loaded in device and
+    stream mode: the same bits as the generated layer with separate stacks"""
+    import gguf_io
+    s = SMALL[0]
+    _say("gguf fused gate+up mode", mode)
+    ref = em.Layer(dev, s, seed=11)
+    _, pf, fused = _fused_desc(dev, ref, s)
+    dev.free(pf)
+    ts = [t for t in gguf_io.layer_tensors(s, seed=11, layer=0) if "gate_exps" not in t[0] and "up_exps" not in t[0]]
+    ts.append(("blk.0.ffn_gate_up_exps.weight", gguf_io.GGML[s.fg], (s.dm, 2 * s.ef, s.ne), fused.tobytes()))
+    path = str(tmp_path / "fused.gguf")
+    gguf_io.write(path, ts)
+    g = dev.lib.llb_gguf_open(path.encode())
+    assert g, dev.lib.llb_hip_last_error()
+    desc = em.MoeLayer(s.dm, s.ne, s.nk, s.ef, s.sf, s.fx | 1 << 12, s.fsg, s.fsu, s.fsd)
+    dev.check(dev.lib.llb_moe_hip_load_layer(g, 0, mode, C.byref(desc)))
+
+    class Lo:
+        pass
+    lo = Lo()
+    lo.desc = desc
+    try:
+        assert desc.U == 0
+        run = em.Runner(dev, s, 1, tier=em.EXACT)
+        for seed in (20, 21, 22):
+            run.gen_inputs(seed)
+            run.forward(ref)
+            y0, i0, w0 = run.outputs()
+            run.forward(lo)
+            y1, i1, w1 = run.outputs()
+            assert np.array_equal(i0, i1) and np.array_equal(w0.view(np.uint32), w1.view(np.uint32))
+            assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32))
+        run.free()
+    finally:
+        ref.free()
+        dev.check(dev.lib.llb_moe_hip_unload_layer(C.byref(desc)))
+        dev.lib.llb_gguf_close(g)
