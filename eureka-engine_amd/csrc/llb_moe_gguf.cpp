@@ -524,23 +524,22 @@ int stream_stage(const llb_moe_layer* L, const uint32_t* d_ids, const uint32_t**
   uint8_t* dev = (uint8_t*)s->dev;
   for (uint32_t j = 0; j < s->nk; j++)
     if (ids[j] >= L->ne) return llb_fail_msg(LLB_HIP_EINVAL, "stream: an expert id out of range");
-  // gathered in the device staging's order (the nk gate experts, the nk up experts, the nk down experts)
-  // in two jobs, gate / up then down, each uploaded as one copy: the pool gathers the down experts while
-  // the copy engine uploads gate / up
-  std::vector<Seg> sv;
-  sv.reserve(2 * s->nk);
-  for (uint32_t j = 0; j < s->nk; j++) sv.push_back({s->map + s->sg + ids[j] * s->esg, gb});
-  for (uint32_t j = 0; ub && j < s->nk; j++) sv.push_back({s->map + s->su + ids[j] * s->esg, ub});
+  // gathered in the device staging's order (the nk gate experts, the nk up experts, the nk down experts),
+  // one job and one upload a stack: the pool gathers a stack while the copy engine uploads the one before
   GatherPool* pool = gather_pool();
-  const uint64_t a = s->nk * (gb + ub);
-  pool->run(pin, sv);
-  if (hipMemcpyAsync(dev, pin, a, hipMemcpyHostToDevice, st) != hipSuccess)
-    return llb_fail_msg(LLB_HIP_EDEVICE, "stream: cannot stage the gate / up experts");
-  sv.clear();
-  for (uint32_t j = 0; j < s->nk; j++) sv.push_back({s->map + s->sd + ids[j] * s->esd, db});
-  pool->run(pin + a, sv);
-  if (hipMemcpyAsync(dev + a, pin + a, s->nk * db, hipMemcpyHostToDevice, st) != hipSuccess)
-    return llb_fail_msg(LLB_HIP_EDEVICE, "stream: cannot stage the down experts");
+  std::vector<Seg> sv;
+  sv.reserve(s->nk);
+  const uint64_t base[3] = {s->sg, s->su, s->sd}, es[3] = {s->esg, s->esg, s->esd}, len[3] = {gb, ub, db};
+  uint64_t at = 0;
+  for (int k = 0; k < 3; k++) {
+    if (!len[k]) continue;  // fused stacks: the up rows travel with the gate rows
+    sv.clear();
+    for (uint32_t j = 0; j < s->nk; j++) sv.push_back({s->map + base[k] + ids[j] * es[k], len[k]});
+    pool->run(pin + at, sv);
+    if (hipMemcpyAsync(dev + at, pin + at, s->nk * len[k], hipMemcpyHostToDevice, st) != hipSuccess)
+      return llb_fail_msg(LLB_HIP_EDEVICE, "stream: cannot stage the experts");
+    at += s->nk * len[k];
+  }
   *slots = s->slots;
   return 0;
 }
