@@ -299,7 +299,7 @@ struct NormIn {
 };
 static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* ids, float* wt, uint8_t* sc,
                  const ExactScratch& s, bool shared_rows = true, TopkArgs* defer = nullptr,
-                 const NormIn* nin = nullptr) {
+                 const NormIn* nin = nullptr, bool dec = false) {
   float* lg = (float*)(sc + s.lg);
   float* gsu = (float*)(sc + s.gsu);
   TreeArgs a{};
@@ -326,7 +326,9 @@ static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* 
   }
   int rc;
   stage_begin(ST_ROUTE);
-  if ((rc = launched(launch_tree_rows(a, ns, g_stream), "router + shared gate / up"))) return rc;
+  if (dec) rc = launched(launch_router(a, 1u << (cdepth(L->dm) - 6), g_stream), "router");
+  else rc = launched(launch_tree_rows(a, ns, g_stream), "router + shared gate / up");
+  if (rc) return rc;
   stage_end(ST_ROUTE);
   TopkArgs k{};
   k.lg = lg;
@@ -540,11 +542,15 @@ int llb_moe_hip_pack(llb_moe_layer* L, llb_dptr buf, size_t bytes) {
   return 0;
 }
 
-// the fused one-launch layer (exact tier, small T) on by default; 0 forces the four-launch path
+// the fused one-launch layer (exact tier, small T). It hung the GPU twice and the cause is not
+// shown, so it stays off: asking for it is refused; 0 (the four-launch path) is accepted.
 static int g_fused = 0;
 static int g_ncu = 0;
 int llb_moe_hip_set_fused(int on) {
-  g_fused = on;
+  if (on)
+    return fail(LLB_HIP_EINVAL,
+                "set_fused: the fused one-launch layer is disabled (it hung the GPU twice; cause not shown)");
+  g_fused = 0;
   return 0;
 }
 int llb_moe_hip_status(llb_dptr scratch, const llb_moe_layer* L, uint32_t T) {
@@ -588,6 +594,91 @@ int llb_moe_hip_forward_norm(const llb_moe_layer* L, uint32_t T, llb_dptr x, llb
   return forward_impl(L, T, h2, x1, y, ids, wt, scratch, scratch_bytes, tier, &nin);
 }
 
+// the one-token decode layer of the exact tier (moe_decode.hip): router; top-k + gate / up + SwiGLU
+// (with the shared expert's gate / up rows); down + combine + residual. It takes dm = 2048, one
+// format for gate and up, at most 16 down tasks (nk + the shared expert), expert widths that are
+// multiples of 128, and 16-aligned stacks.
+static bool dec_ok(const llb_moe_layer* L) {
+  const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15, fz = L->fx >> 12 & 1;
+  const uint64_t rbg = row_bytes(fg, L->dm);
+  const uint64_t U = fz ? L->G + (uint64_t)L->ef * rbg : L->U;
+  auto a16 = [](uint64_t p) { return p % 16 == 0; };
+  if (L->dm != 2048 || fg != fu || L->nk + (L->sf ? 1 : 0) > 16 || L->ef % 128 || L->ef > 4096) return false;
+  // the gate / up launch spreads the shared expert's features over its blocks, at most 15 a block
+  if (L->sf > 15 * (L->nk * L->ef / 16)) return false;
+  if (!a16(L->G) || !a16(U) || !a16(L->D) || !a16(L->router)) return false;
+  if (L->sf && (L->sf % 128 || L->sf > 4096 || !a16(L->SG) || !a16(L->SU) || !a16(L->SD) || !a16(L->shgate)))
+    return false;
+  return true;
+}
+static int decode_forward(const llb_moe_layer* L, const float* h2, const float* x1, float* y, uint32_t* ids,
+                          float* wt, uint8_t* sc, const ExactScratch& s, const NormIn* nin) {
+  const uint32_t fg = L->fx & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
+  TopkArgs tk{};
+  int rc = route(L, 1, h2, ids, wt, sc, s, false, &tk, nin, true);
+  if (rc) return rc;
+  const uint64_t rbg = row_bytes(fg, L->dm);
+  DecGuArgs g{};
+  g.G = dp<uint8_t>(L->G);
+  g.U = fz ? g.G + (uint64_t)L->ef * rbg : dp<uint8_t>(L->U);
+  g.es = (uint64_t)(fz ? 2 : 1) * L->ef * rbg;
+  g.SG = L->sf ? dp<uint8_t>(L->SG) : nullptr;
+  g.SU = L->sf ? dp<uint8_t>(L->SU) : nullptr;
+  g.dm = L->dm;
+  g.ef = L->ef;
+  g.nk = L->nk;
+  g.sf = L->sf;
+  g.h2 = h2;
+  g.act = (float*)(sc + s.act);
+  g.gsu = (float*)(sc + s.gsu);
+  g.sa = (float*)(sc + s.sa);
+  g.tk = tk;
+  stage_begin(ST_GU);
+  if ((rc = launched(launch_gu_dec(g, fg, L->sf ? L->fsg : 0, g_stream), "top-k + expert gate/up (decode)"))) return rc;
+  stage_end(ST_GU);
+  DecDnArgs d{};
+  d.D = dp<uint8_t>(L->D);
+  d.rbd = row_bytes(fd, L->ef);
+  d.SD = L->sf ? dp<uint8_t>(L->SD) : nullptr;
+  d.rbs = L->sf ? row_bytes(L->fsd, L->sf) : 0;
+  d.dm = L->dm;
+  d.ef = L->ef;
+  d.nk = L->nk;
+  d.sf = L->sf;
+  d.act = g.act;
+  d.sa = g.sa;
+  d.ids = ids;
+  d.wt = wt;
+  d.sgo = tk.sgo;
+  d.x1 = x1;
+  d.y = y;
+  stage_begin(ST_DN);
+  int lr = launch_dn_dec(d, fd, L->sf ? L->fsd : 0, g_stream);
+  if (lr) {  // more down tasks or wider rows than its LDS holds: the general down kernel, same inputs
+    DnArgs o{};
+    o.D = d.D;
+    o.rbd = d.rbd;
+    o.SD = d.SD;
+    o.rbs = d.rbs;
+    o.dm = d.dm;
+    o.ef = d.ef;
+    o.nk = d.nk;
+    o.sf = d.sf;
+    o.rw = dn_rows(L->nk, L->ef, L->sf);
+    o.act = d.act;
+    o.gsu = g.gsu;
+    o.ids = ids;
+    o.wt = wt;
+    o.sgo = d.sgo;
+    o.x1 = x1;
+    o.y = y;
+    lr = launch_dn_exact(o, fd, L->sf ? L->fsd : 0, 1, g_stream);
+  }
+  rc = launched(lr, "expert down + combine (decode)");
+  stage_end(ST_DN);
+  return rc;
+}
+
 static int forward_impl(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dptr x1, llb_dptr y, llb_dptr ids,
                         llb_dptr wt, llb_dptr scratch, size_t scratch_bytes, int tier, const NormIn* nin) {
   int rc = check_layer(L, tier);
@@ -611,6 +702,8 @@ static int forward_impl(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
   const bool streamed = L->res == LLB_MOE_RES_STREAM;
   if (streamed && (tier != LLB_MOE_EXACT || T != 1 || g_capturing))
     return fail(LLB_HIP_EINVAL, "stream residency: the exact tier, one token, outside graph capture");
+  if (tier == LLB_MOE_EXACT && T == 1 && !streamed && dec_ok(L))
+    return decode_forward(L, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt), sc, s, nin);
   TopkArgs tk{};
   const bool fuse_topk = (tier == LLB_MOE_Q8 || fg == fu) && T == 1 && !streamed;
   // the q8 tier computes the shared gate / up rows in its own gate / up launch (int8 dots)

@@ -31,6 +31,11 @@ __device__ unsigned long long moe_blk_t[4][4096][2];
   do { if (threadIdx.x == 0 && blockIdx.x < 4096 && blockIdx.y == 0) moe_blk_t[k][blockIdx.x][i] = __builtin_amdgcn_s_memrealtime(); } while (0)
 // stamp i once v has arrived (the asm takes v as an input, so the wait for it comes first)
 #define PHASE_AFTER(i, v) do { __asm__ volatile("" :: "v"(v)); PHASE(i); } while (0)
+// the stamps to the host: phase [64], blk [4][4096][2]
+extern "C" int moe_phase_read(unsigned long long* phase, unsigned long long* blk) {
+  if (hipMemcpyFromSymbol(phase, HIP_SYMBOL(moe_phase_t), sizeof moe_phase_t) != hipSuccess) return -1;
+  return hipMemcpyFromSymbol(blk, HIP_SYMBOL(moe_blk_t), sizeof moe_blk_t) == hipSuccess ? 0 : -1;
+}
 #else
 #define PHASE_AFTER(i, v) do {} while (0)
 #define PHASE(i) do {} while (0)

@@ -73,6 +73,38 @@ struct DnArgs {
   float* y;
 };
 
+// the one-token decode layer (moe_decode.hip)
+struct DecGuArgs {
+  const uint8_t *G, *U;   // routed gate / up rows (one format, dm = 2048 columns, 16-aligned)
+  uint64_t es;            // expert stride of G and U in bytes
+  const uint8_t *SG, *SU; // the shared expert's gate / up rows (tree order), null when sf == 0
+  uint32_t dm, ef, nk, sf;
+  uint32_t nrb;           // routed blocks (the shared expert's follow)
+  const float* h2;        // [dm]
+  float* act;             // [nk][ef] (SwiGLU applied)
+  float* gsu;             // [2 sf]: shared gate, then up dots
+  float* sa;              // [sf]: the shared expert's SwiGLU
+  TopkArgs tk;            // the token's logits in, ids / wt / sgo out
+};
+struct DecDnArgs {
+  const uint8_t* D;
+  uint64_t rbd;
+  const uint8_t* SD;
+  uint64_t rbs;
+  uint32_t dm, ef, nk, sf;
+  const float* act;  // [nk][ef]
+  const float* sa;   // [sf]: the shared expert's SwiGLU
+  const uint32_t* ids;
+  const float* wt;
+  const float* sgo;
+  const float* x1;  // nullable
+  float* y;
+  uint32_t stage_bytes, xw_bytes;  // LDS a wave stages its rows / activations in, set by the launcher
+};
+int launch_router(const TreeArgs& a, uint32_t nq, hipStream_t st);
+int launch_gu_dec(DecGuArgs a, uint32_t f, uint32_t fs, hipStream_t st);
+int launch_dn_dec(DecDnArgs a, uint32_t fd, uint32_t fs, hipStream_t st);
+
 struct FusedArgs {
   TreeArgs tr;
   TopkArgs tk;

@@ -122,11 +122,12 @@ int llb_moe_hip_forward_norm(const llb_moe_layer* L, uint32_t T, llb_dptr x, llb
                              llb_dptr x1, llb_dptr h2, llb_dptr y, llb_dptr ids, llb_dptr wt, llb_dptr scratch,
                              size_t scratch_bytes, int tier);
 
-/* The exact tier at T <= 8 runs a layer as one persistent launch (the "fused" path; the four-launch
- * sequence otherwise). The fused path keeps 6 counters in the scratch, which must be zero before
- * its first use (llb_hip_alloc_zero gives that) and which every launch leaves zero. on = 0 forces
- * the four-launch path (same bits). status returns LLB_HIP_EDEVICE (and clears it) when a fused
- * launch on that scratch had a bounded wait time out. No counterpart in the reference. */
+/* The fused one-launch layer (k_fused: the four stages as work items of one persistent launch with
+ * completion counters between phases) is disabled: it hung the GPU twice and the cause is not shown.
+ * set_fused(0) is accepted (the three / four-launch path, the only one that runs); set_fused(on != 0)
+ * returns LLB_HIP_EINVAL with a message naming the hang. status reads the fused path's timeout flag
+ * in a scratch (LLB_HIP_EDEVICE, cleared, when set); with the path disabled it is never set.
+ * No counterpart in the reference. */
 int llb_moe_hip_set_fused(int on);
 int llb_moe_hip_status(llb_dptr scratch, const llb_moe_layer* L, uint32_t T);
 

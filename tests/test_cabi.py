@@ -84,3 +84,11 @@ def test_forward_refuses_buffers_tier_and_scratch():
     rc = lib.llb_moe_hip_forward_norm(C.byref(L), 1, DUMMY, 0, DUMMY, 1e-6, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, DUMMY,
                                       1 << 30, em.EXACT)
     assert rc == -1 and b"input-step" in lib.llb_hip_last_error()
+
+
+def test_fused_path_is_refused():
+    """the fused one-launch layer hung the GPU and its cause is not shown: asking for it is an error"""
+    lib = em.load()
+    assert lib.llb_moe_hip_set_fused(1) == -1
+    assert b"disabled" in lib.llb_hip_last_error() and b"hung" in lib.llb_hip_last_error()
+    assert lib.llb_moe_hip_set_fused(0) == 0
