@@ -633,6 +633,14 @@ static int decode_forward(const llb_moe_layer* L, const float* h2, const float* 
   g.gsu = (float*)(sc + s.gsu);
   g.sa = (float*)(sc + s.sa);
   g.tk = tk;
+  g.D = dp<uint8_t>(L->D);
+  g.rbd = row_bytes(fd, L->ef);
+  g.SD = L->sf ? dp<uint8_t>(L->SD) : nullptr;
+  g.rbs = L->sf ? row_bytes(L->fsd, L->sf) : 0;
+  g.ndb = (L->dm + 7) / 8;
+#ifdef MOE_DEC_STAMPS
+  g.stamps = g_dec_stamps;
+#endif
   stage_begin(ST_GU);
   if ((rc = launched(launch_gu_dec(g, fg, L->sf ? L->fsg : 0, g_stream), "top-k + expert gate/up (decode)"))) return rc;
   stage_end(ST_GU);
@@ -652,6 +660,9 @@ static int decode_forward(const llb_moe_layer* L, const float* h2, const float* 
   d.sgo = tk.sgo;
   d.x1 = x1;
   d.y = y;
+#ifdef MOE_DEC_STAMPS
+  d.stamps = g_dec_stamps;
+#endif
   stage_begin(ST_DN);
   int lr = launch_dn_dec(d, fd, L->sf ? L->fsd : 0, g_stream);
   if (lr) {  // more down tasks or wider rows than its LDS holds: the general down kernel, same inputs

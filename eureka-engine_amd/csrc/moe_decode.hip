@@ -29,13 +29,14 @@
 // per-block wall-clock stamps for latency studies (100 MHz): a build that defines MOE_PHASE_T records
 // stamp i of block b of thread 0 (and of thread 64, stamps >= 8 of k_gu_dec) in dec_stamp[i][b]; the
 // library build compiles them away
-#ifdef MOE_PHASE_T
-__device__ unsigned long long dec_stamp[32][1024];
-#define DSTAMP(i) do { if ((threadIdx.x == 0 || ((i) >= 8 && (i) < 16 && threadIdx.x == 64)) && blockIdx.x < 1024) \
-    dec_stamp[i][blockIdx.x] = __builtin_amdgcn_s_memrealtime(); } while (0)
-extern "C" int moe_dec_stamp_read(unsigned long long* out) {
-  return hipMemcpyFromSymbol(out, HIP_SYMBOL(dec_stamp), sizeof dec_stamp) == hipSuccess ? 0 : -1;
-}
+#ifdef MOE_DEC_STAMPS
+// stamp i of block b (thread 0; stamps 8..15 of k_gu_dec from thread 960, its last wave) in shader clocks
+// (s_memtime), into the buffer the arguments carry (dec_stamps: [32][1024] u64, set by the host)
+#define DSTAMP(i) do { if ((threadIdx.x == 0 || ((i) >= 8 && (i) < 16 && threadIdx.x == 960)) && blockIdx.x < 1024 && a.stamps) { \
+    __builtin_amdgcn_sched_barrier(0); a.stamps[(i) * 1024 + blockIdx.x] = __builtin_readcyclecounter(); __builtin_amdgcn_sched_barrier(0); } } while (0)
+// the host side: the decode launches pass this buffer
+unsigned long long* g_dec_stamps = nullptr;
+extern "C" void moe_dec_set_stamps(unsigned long long* p) { g_dec_stamps = p; }
 #else
 #define DSTAMP(i) do {} while (0)
 #endif
@@ -332,32 +333,50 @@ DEV TopkLane topk_wave(const float* lg, u32 ne, u32 nk) {
   }
   return out;
 }
-// The same routing by a block of 1024 threads (ne <= 512; the gate / up block's waves are idle until
-// it is known): expert e on thread e for the softmax (group sums in order, as above); the 64-bit keys
-// (kb << 32 | ~e: a larger key is a larger p, then a lower index) go to LDS; thread t counts the keys
-// of segment t / NP (NP = 256 or 512 keys padded with zeros, 1024 / NP segments) larger than key
-// t % NP; the segment counts add up to each key's rank, and ranks below nk name the slots. A key
-// without a real p (past ne, or NaN) fills no slot; unfilled slots keep expert 0, p 0.
-// LDS: key [NP] u64, cnt [1024] u32, red [64] f32, slots [64] u32 + [64] f32. Every thread calls it;
-// thread j < nk returns slot j.
-constexpr u32 TKB_LDS = 512 * 8 + 1024 * 4 + 64 * 4 + 64 * 8;
+// The same routing by a block of 1024 threads (ne <= 512, nk <= 16; the gate / up block's waves are
+// idle until it is known). Expert e on thread e for the softmax (group sums in order, as above). The
+// 64-bit keys kb << 32 | ~e (a larger key is a larger p, then a lower index; all distinct) go to LDS.
+// A key's place in its 64-expert group is the count of the group's larger keys, four threads a key
+// (16 compares each); only a group's first nk can be in the top nk, so places below nk become
+// candidates, in place order. A candidate's rank is its place plus the count of larger candidates of
+// the other groups, again spread over threads (one (candidate, group) pair a thread). Ranks below nk
+// name the slots. A key without a real p (past ne, or NaN) fills no slot; unfilled slots keep
+// expert 0, p 0.
+// LDS: keys [512] u64, candidates [8 x 16] u64, counts [1024] u8 (as u32 words), red [64] f32,
+// slots [64] u32 + [64] f32 (slot j's expert at sid[j] when it returns). Every thread calls it; thread
+// j < nk returns slot j.
+constexpr u32 TKB_LDS = 512 * 8 + 128 * 8 + 1024 + 64 * 4 + 64 * 8;
+#ifdef MOE_DEC_STAMPS
+#define TSTAMP(i) do { if (threadIdx.x == 0 && stamps) { __builtin_amdgcn_sched_barrier(0); stamps[(i) * 1024 + blockIdx.x] = __builtin_readcyclecounter(); __builtin_amdgcn_sched_barrier(0); } } while (0)
+#else
+#define TSTAMP(i) do {} while (0)
+#endif
 template <u32 NP>
-DEV TopkLane topk_block(const float* lg, u32 ne, u32 nk, u8* tl) {
-  unsigned long long* key = (unsigned long long*)tl;
-  u32* cnt = (u32*)(tl + 512 * 8);
-  float* red = (float*)(tl + 512 * 8 + 1024 * 4);
+DEV TopkLane topk_block(const float* lg, u32 ne, u32 nk, u8* tl, float* xs, float4 xv,
+                        unsigned long long* stamps = nullptr) {
+  static_assert(NP == 256 || NP == 512, "64-expert groups, 1024 threads");
+  unsigned long long* key = (unsigned long long*)tl;             // [NP]
+  unsigned long long* cand = key + 512;                          // [NW][16]
+  u8* cnt = (u8*)(cand + 128);                                   // [1024]
+  float* red = (float*)(cnt + 1024);
   u32* sid = (u32*)(red + 64);
   float* sp = (float*)(sid + 64);
   const u32 t = threadIdx.x, L = t & 63, w = t >> 6;
-  constexpr u32 NW = NP / 64;  // waves that hold experts
+  constexpr u32 NW = NP / 64;       // expert groups (waves that hold experts)
+  constexpr u32 PK = 1024 / NP;     // threads a key for its place (4 or 2)
+  constexpr u32 PZ = 64 / PK;       // keys each of them compares (16 or 32)
   float v = 0.0f;
   if (t < NP) {
     v = t < ne ? lg[t] : 0.0f;
+    __asm__ volatile("" :: "v"(v));
+    TSTAMP(11);
     const float mw = wave_fmax(t < ne ? v : bits_f(0xFF800000u));
     if (L == 0) red[w] = mw;
   }
   if (t < 64) { sid[t] = 0u; sp[t] = 0.0f; }
   __syncthreads();
+  TSTAMP(12);
+  if (t < 512) *(float4*)(xs + xpad(4 * t)) = xv;
   float mx = red[0];
 #pragma unroll
   for (u32 i = 1; i < NW; i++) mx = fmaxf(mx, red[i]);
@@ -367,35 +386,58 @@ DEV TopkLane topk_block(const float* lg, u32 ne, u32 nk, u8* tl) {
     if ((L & 31) == 0) red[16 + (t >> 5)] = sg;  // group t / 32
   }
   __syncthreads();
-  float tot = 0.0f;
-  for (u32 g = 0; g < 2 * NW; g++) tot = tot + red[16 + g];  // groups past ne sum to +0
-  const float inv = 1.0f / tot;
   if (t < NP) {
-    const float p = v * inv;
+    float tot = 0.0f;
+#pragma unroll
+    for (u32 g = 0; g < 2 * NW; g++) tot = tot + red[16 + g];  // groups past ne sum to +0
+    const float p = v * (1.0f / tot);
     const u32 kb = (t < ne && p >= 0.0f) ? __float_as_uint(p) + 1u : 0u;
     key[t] = ((u64)kb << 32) | (0xFFFFFFFFu - t);
   }
   __syncthreads();
-  {
-    constexpr u32 S = 1024 / NP, Z = NP / S;
+  TSTAMP(13);
+  {  // key j's larger keys among part s of its group
     const u32 j = t % NP, sg = t / NP;
     const u64 mine = key[j];
-    const u64* kp = (const u64*)key + sg * Z;
+    const u64* kp = (const u64*)key + (j & ~63u) + sg * PZ;
     u32 c = 0;
-#pragma unroll 8
-    for (u32 i = 0; i < Z; i++) c += kp[i] > mine ? 1u : 0u;
-    cnt[t] = c;
+#pragma unroll
+    for (u32 i = 0; i < PZ; i++) c += kp[i] > mine ? 1u : 0u;
+    cnt[sg * NP + j] = (u8)c;
   }
   __syncthreads();
+  const u32 nc = min(nk, 16u);  // candidates a group
   if (t < NP) {
-    constexpr u32 S = 1024 / NP;
-    u32 rk = 0;
+    u32 r = 0;
 #pragma unroll
-    for (u32 s2 = 0; s2 < S; s2++) rk += cnt[s2 * NP + t];
-    const u64 mine = key[t];
-    if (rk < nk && (mine >> 32) != 0ull) {
-      sid[rk] = t;
-      sp[rk] = __uint_as_float((u32)(mine >> 32) - 1u);
+    for (u32 s2 = 0; s2 < PK; s2++) r += cnt[s2 * NP + t];
+    if (r < nc) cand[w * 16 + r] = key[t];
+  }
+  __syncthreads();
+  TSTAMP(14);
+  // candidate c = (group g, place q) against group o: thread (g, q, o), 16 x NW x NW <= 1024 threads
+  {
+    const u32 g = t / (16 * NW), q = (t / NW) % 16, o = t % NW;
+    u32 c = 0;
+    if (g < NW && q < nc && o != g) {
+      const u64 mine = cand[g * 16 + q];
+#pragma unroll
+      for (u32 i = 0; i < 16; i++) c += (i < nc && cand[o * 16 + i] > mine) ? 1u : 0u;
+    }
+    if (t < 16 * NW * NW) cnt[t] = (u8)c;
+  }
+  __syncthreads();
+  if (t < 16 * NW) {
+    const u32 g = t / 16, q = t % 16;
+    if (q < nc) {
+      u32 rk = q;
+#pragma unroll
+      for (u32 o = 0; o < NW; o++) rk += cnt[t * NW + o];
+      const u64 mine = cand[g * 16 + q];
+      if (rk < nk && (mine >> 32) != 0ull) {
+        sid[rk] = 0xFFFFFFFFu - (u32)mine;
+        sp[rk] = __uint_as_float((u32)(mine >> 32) - 1u);
+      }
     }
   }
   __syncthreads();
@@ -424,7 +466,6 @@ template <u32 NQ>
 __global__ void __launch_bounds__(256) k_router(TreeArgs a) {
   constexpr u32 QW = NQ / 4;
   __shared__ float part[4];
-  DSTAMP(24);
   const u32 tid = threadIdx.x, L = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const u32 nl4 = a.cols / 4;
   // row r of segment 0 (router) or 1 (the shared gate row); fields picked by selects, not an index
@@ -502,7 +543,6 @@ __global__ void __launch_bounds__(256) k_router(TreeArgs a) {
     const float v = (part[0] + part[1]) + (part[2] + part[3]);
     out[r] = bias ? v + bias[r] : v;
   }
-  DSTAMP(25);
 }
 
 int launch_router(const TreeArgs& a, u32 nq, hipStream_t st) {
@@ -523,6 +563,7 @@ int launch_router(const TreeArgs& a, u32 nq, hipStream_t st) {
 // LDS of k_gu_dec (bytes): x (dm = 2048, padded) | routing: ids [64], candidates [64] u64 | the pairs'
 // gate / up dots [32][2] | per wave: one staged pair (gate row | up row), the pair's leaves [2][512]
 constexpr u32 DEC_DM = 2048;
+constexpr u32 DN_RB_G = 8;  // outputs a down block takes (DN_RB below)
 // row bytes of 2048 columns
 static constexpr u32 rb2048(u32 f) {
   return f == FM_Q8_0 ? 2176u : f == FM_Q4_K ? 1152u : f == FM_Q5_K ? 1408u : f == FM_Q6_K ? 1680u : 0u;
@@ -533,7 +574,8 @@ constexpr u32 DEC_GU = 32 * 2 * 4;                   // 256
 constexpr u32 DEC_LV = 2 * (DEC_DM / 4) * 4;         // 4096
 constexpr u32 GU_WAVES = 16;
 constexpr u32 gu_wave_lds(u32 rb) { return 2 * rb + DEC_LV; }
-constexpr u32 gu_lds(u32 rb) { return DEC_XS + DEC_TK + DEC_GU + GU_WAVES * gu_wave_lds(rb); }
+constexpr u32 DEC_TKB = TKB_LDS;  // topk_block's LDS
+constexpr u32 gu_lds(u32 rb) { return DEC_XS + DEC_TK + DEC_GU + DEC_TKB + GU_WAVES * gu_wave_lds(rb); }
 
 // one row pair, staged by the wave: the 16-byte chunks of [gate row | up row] (RB bytes each, 16-aligned),
 // chunk c = 64 k + L, loaded coalesced into registers (lanes past the end re-load the last chunk)
@@ -557,9 +599,7 @@ template <u32 RB> struct PairChunks {
 // the pair's dots on lane 0 (gate) and lane 32 (up): moe_dot's stride order (routed rows), or the
 // engine tree (the shared expert's rows)
 template <u32 F, u32 RB, bool TREE>
-DEV float pair_dots(const PairChunks<RB>& pc, u8* stage, float* lv, const float* xs, u32 L) {
-  pc.store(stage, L);
-  WAVE_FENCE();
+DEV float pair_compute(u8* stage, float* lv, const float* xs, u32 L) {
   const u32 h = L >> 5, q = L & 31;
   float lf[16];
   leaves64<F>(stage + h * RB, q, xs, lf);
@@ -570,6 +610,12 @@ DEV float pair_dots(const PairChunks<RB>& pc, u8* stage, float* lv, const float*
     WAVE_FENCE();
     return chain32c<DEC_DM / 128>(lv + h * (DEC_DM / 4), q);
   }
+}
+template <u32 F, u32 RB, bool TREE>
+DEV float pair_dots(const PairChunks<RB>& pc, u8* stage, float* lv, const float* xs, u32 L) {
+  pc.store(stage, L);
+  WAVE_FENCE();
+  return pair_compute<F, RB, TREE>(stage, lv, xs, L);
 }
 
 // A block of 16 waves takes 16 consecutive features of one slot, one a wave: the feature's gate row on
@@ -588,7 +634,8 @@ __global__ void __launch_bounds__(1024) k_gu_dec(DecGuArgs a) {
   float* gus = (float*)(sm + DEC_XS + DEC_TK);
   const u32 tid = threadIdx.x, L = tid & 63;
   const u32 w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  u8* stage = sm + DEC_XS + DEC_TK + DEC_GU + w * gu_wave_lds(RBX);
+  u8* tkb = sm + DEC_XS + DEC_TK + DEC_GU;
+  u8* stage = tkb + DEC_TKB + w * gu_wave_lds(RBX);
   float* lv = (float*)(stage + 2 * RBX);
   const u32 bps = a.ef / GU_WAVES, slot = blockIdx.x / bps, f = (blockIdx.x % bps) * GU_WAVES + w;
   // the shared feature this wave takes (waves 1 ..), or none
@@ -600,22 +647,33 @@ __global__ void __launch_bounds__(1024) k_gu_dec(DecGuArgs a) {
   // x, loaded now (its latency overlaps the routing's) and stored to LDS, padded, once routed
   const float4 xv = tid < 512 ? ((const float4*)a.h2)[tid] : make_float4(0.f, 0.f, 0.f, 0.f);
   TopkLane tl{0u, 0.0f};
+  const u32* ids_s = tk_id;  // the token's experts by rank, in LDS
+  bool routed_ok = false;
   if constexpr (NI <= 8) {
-    // the routing by the whole block (its LDS is the staging area, not yet in use)
-    tl = topk_block<64 * NI>(a.tk.lg, a.tk.ne, a.tk.nk, sm + DEC_XS + DEC_TK + DEC_GU);
-    if (tid < a.tk.nk) tk_id[tid] = tl.id;
-  } else {
+    if (a.tk.nk <= 16) {  // the routing by the whole block; x goes to LDS on the way; its last barrier
+                          // publishes the slots
+#ifdef MOE_DEC_STAMPS
+      tl = topk_block<64 * NI>(a.tk.lg, a.tk.ne, a.tk.nk, tkb, xs, xv, a.stamps);
+#else
+      tl = topk_block<64 * NI>(a.tk.lg, a.tk.ne, a.tk.nk, tkb, xs, xv);
+#endif
+      ids_s = (const u32*)(tkb + 512 * 8 + 128 * 8 + 1024 + 64 * 4);
+      routed_ok = true;
+    }
+  }
+  if (!routed_ok) {  // the one-wave routing (more experts, or more than 16 slots)
     if (w == 0) {
       tl = topk_wave<NI>(a.tk.lg, a.tk.ne, a.tk.nk);
       if (L < a.tk.nk) tk_id[L] = tl.id;
     }
+    if (tid < 512) *(float4*)(xs + xpad(4 * tid)) = xv;
+    __syncthreads();
+    ids_s = tk_id;
   }
   DSTAMP(1);
-  if (tid < 512) *(float4*)(xs + xpad(4 * tid)) = xv;
-  __syncthreads();
   DSTAMP(2);
   DSTAMP(8);
-  const u64 e = tk_id[slot % a.nk];
+  const u64 e = ids_s[slot % a.nk];
   PairChunks<RB> pc;
   pc.load(a.G + e * a.es + (u64)f * RB, a.U + e * a.es + (u64)f * RB, L);
   DSTAMP(3);
@@ -628,7 +686,30 @@ __global__ void __launch_bounds__(1024) k_gu_dec(DecGuArgs a) {
       WAVE_FENCE();
     }
   }
-  const float sv = pair_dots<F, RB, false>(pc, stage, lv, xs, L);
+  pc.store(stage, L);
+  WAVE_FENCE();
+  DSTAMP(7);
+  DSTAMP(10);
+  // the down launch's rows for its block b3 = blockIdx (same XCD, so the same L2): task w's DN_RB rows,
+  // one dword a 128-byte line, issued once this wave's own rows have landed. The load is an asm
+  // statement, so the compiler neither moves it nor counts it in its waits; the data is never used,
+  // only waited for at the end.
+  u32 touch = 0;
+  {
+    // waves past the tasks, and grids where this block has no down block, touch expert 0's first line
+    const u32 b3 = blockIdx.x < a.ndb ? blockIdx.x : 0u;
+    const bool sh = a.SD && w == a.nk;
+    const u64 rb = sh ? a.rbs : a.rbd;
+    const u8* base = sh ? a.SD + (u64)(DN_RB_G * b3) * rb
+                        : a.D + ((u64)ids_s[min(w, a.nk - 1)] * a.dm + DN_RB_G * b3) * rb;
+    // (pointer arithmetic, not integers, so the load stays a global load: a flat one would also count
+    // against the LDS wait counter)
+    const u8* lo = base - ((u32)(uintptr_t)base & 127u);
+    const bool live = w < a.nk + (a.SD ? 1u : 0u) && lo + 128 * L < base + DN_RB_G * rb;
+    touch = *(const u32*)(live ? lo + 128 * L : a.D);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const float sv = pair_compute<F, RB, false>(stage, lv, xs, L);
   if (L == 0) gus[2 * w] = sv;
   if (L == 32) gus[2 * w + 1] = sv;
   DSTAMP(4);
@@ -662,6 +743,8 @@ __global__ void __launch_bounds__(1024) k_gu_dec(DecGuArgs a) {
       }
     }
   }
+  wait_vm0();
+  __asm__ volatile("" :: "v"(touch));
   DSTAMP(6);
 }
 
@@ -673,7 +756,7 @@ __global__ void __launch_bounds__(1024) k_gu_dec(DecGuArgs a) {
 // A lane decodes 64-column group q of one row (LPR = cols / 64 lanes a row, 64 / LPR rows a pass);
 // part[DN_RB][16] holds the dots; threads < DN_RB combine them: ((v0 wt0 + v1 wt1 + ...) in rank
 // order + hv sgo) + x1.
-constexpr u32 DN_RB = 8;
+constexpr u32 DN_RB = DN_RB_G;
 constexpr u32 DN_PART = DN_RB * 16 * 4;                 // part, bytes
 // a wave's LDS: staged rows | its activations (padded) | leaves [<= 1024]
 DEV u32 dn_wave_lds(const DecDnArgs& a) { return a.stage_bytes + a.xw_bytes + 4096; }

@@ -85,6 +85,15 @@ struct DecGuArgs {
   float* gsu;             // [2 sf]: shared gate, then up dots
   float* sa;              // [sf]: the shared expert's SwiGLU
   TopkArgs tk;            // the token's logits in, ids / wt / sgo out
+  // the down launch's rows, touched into this XCD's L2 for the down block of the same XCD (0: none)
+  const uint8_t* D;
+  uint64_t rbd;
+  const uint8_t* SD;
+  uint64_t rbs;
+  uint32_t ndb;           // down blocks (DN_RB outputs each)
+#ifdef MOE_DEC_STAMPS
+  unsigned long long* stamps;
+#endif
 };
 struct DecDnArgs {
   const uint8_t* D;
@@ -100,7 +109,13 @@ struct DecDnArgs {
   const float* x1;  // nullable
   float* y;
   uint32_t stage_bytes, xw_bytes;  // LDS a wave stages its rows / activations in, set by the launcher
+#ifdef MOE_DEC_STAMPS
+  unsigned long long* stamps;
+#endif
 };
+#ifdef MOE_DEC_STAMPS
+extern unsigned long long* g_dec_stamps;
+#endif
 int launch_router(const TreeArgs& a, uint32_t nq, hipStream_t st);
 int launch_gu_dec(DecGuArgs a, uint32_t f, uint32_t fs, hipStream_t st);
 int launch_dn_dec(DecDnArgs a, uint32_t fd, uint32_t fs, hipStream_t st);
