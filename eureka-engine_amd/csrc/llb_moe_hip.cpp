@@ -326,6 +326,9 @@ static int route(const llb_moe_layer* L, uint32_t T, const float* h2, uint32_t* 
   }
   int rc;
   stage_begin(ST_ROUTE);
+#ifdef MOE_DEC_STAMPS
+  a.stamps = g_dec_stamps;
+#endif
   if (dec) rc = launched(launch_router(a, 1u << (cdepth(L->dm) - 6), g_stream), "router");
   else rc = launched(launch_tree_rows(a, ns, g_stream), "router + shared gate / up");
   if (rc) return rc;

@@ -466,6 +466,7 @@ template <u32 NQ>
 __global__ void __launch_bounds__(256) k_router(TreeArgs a) {
   constexpr u32 QW = NQ / 4;
   __shared__ float part[4];
+  DSTAMP(24);
   const u32 tid = threadIdx.x, L = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const u32 nl4 = a.cols / 4;
   // row r of segment 0 (router) or 1 (the shared gate row); fields picked by selects, not an index
@@ -543,6 +544,7 @@ __global__ void __launch_bounds__(256) k_router(TreeArgs a) {
     const float v = (part[0] + part[1]) + (part[2] + part[3]);
     out[r] = bias ? v + bias[r] : v;
   }
+  DSTAMP(25);
 }
 
 int launch_router(const TreeArgs& a, u32 nq, hipStream_t st) {

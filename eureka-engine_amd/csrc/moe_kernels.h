@@ -41,6 +41,9 @@ struct TreeArgs {
   float eps;
   float* x1o;
   float* h2o;
+#ifdef MOE_DEC_STAMPS
+  unsigned long long* stamps;
+#endif
 };
 struct TopkArgs {
   const float* lg;  // [T][lstride]: ne logits, then the shared gate's when has_sg
