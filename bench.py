@@ -41,9 +41,9 @@ def measured_traffic(workload, stage, applies=True):
 # kernel (rocprofv3 name prefix) -> (workload, stage) for the PMC passes run with --legs prefill,prefill_k;
 # the GEMM's first template argument is the weight format (1 Q8_0, 3 Q4_K, 4 Q6_K), its second the mode
 TRAFFIC_KERNELS = {
-    "k_tree_rows<": ("c2_decode", "route"),
-    "k_gu_topk<": ("c2_decode", "gate_up"),
-    "k_dn_lane<": ("c2_decode", "down"),
+    "k_router<": ("c2_decode", "route"),
+    "k_gu_dec<": ("c2_decode", "gate_up"),
+    "k_dn_dec<": ("c2_decode", "down"),
     "k_moe_gemm3<1u, 0u, true>": ("c1_prefill_2048", "gate_up"),
     "k_moe_gemm3<1u, 1u, true>": ("c1_prefill_2048", "down"),
     "k_moe_gemm3<3u, 0u, true>": ("c1k_prefill_2048", "gate_up"),
@@ -87,6 +87,17 @@ def traffic_from(d):
                      "the factors from 256 MiB device-to-device copies (bench.py --copy-calib) profiled the same way",
            "fetch_factor": round(ff, 4), "write_factor": round(wf, 4),
            "calibration_kib": {"fetch": cf, "write": cw}, "kib_per_dispatch": {}}
+    # kernels the passes did not see keep their earlier figures (a pass may cover decode or prefill only)
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            old = json.load(f)
+        for k, v in old.get("kib_per_dispatch", {}).items():
+            if k in TRAFFIC_KERNELS and k not in fe:
+                out["kib_per_dispatch"][k] = v
+                wl, st = TRAFFIC_KERNELS[k]
+                out.setdefault(wl, {})[st] = old[wl][st]
+    except (OSError, KeyError, ValueError):
+        pass
     for k, (wl, st) in TRAFFIC_KERNELS.items():
         if k in fe and k in wr:
             out.setdefault(wl, {})[st] = int(round((fe[k] * ff + wr[k] * wf) * 1024))
@@ -96,15 +107,22 @@ def traffic_from(d):
     print(json.dumps(out, indent=1))
 
 
-def stage_bytes(shape, T=1):
-    """algorithmic HBM bytes per launch of each stage for T = 1 decode (every selected expert distinct)."""
+def stage_bytes(shape, T=1, shared_in_gu=True):
+    """algorithmic HBM bytes per launch of each stage for T = 1 decode (every selected expert distinct).
+    shared_in_gu: the one-token decode kernels read the shared expert's gate / up rows in the gate / up
+    launch (k_gu_dec); the general path reads them in the router launch."""
     s = shape
     rbg, rbu, rbd = em.row_bytes(s.fg, s.dm), em.row_bytes(s.fu, s.dm), em.row_bytes(s.fd, s.ef)
     route = s.ne * s.dm * 4
     gate_up = s.nk * s.ef * (rbg + rbu)
     down = s.nk * s.dm * rbd
     if s.sf:
-        route += s.dm * 4 + s.sf * (em.row_bytes(s.fsg, s.dm) + em.row_bytes(s.fsu, s.dm))
+        sgu = s.sf * (em.row_bytes(s.fsg, s.dm) + em.row_bytes(s.fsu, s.dm))
+        route += s.dm * 4
+        if shared_in_gu:
+            gate_up += sgu
+        else:
+            route += sgu
         down += s.dm * em.row_bytes(s.fsd, s.sf)
     return {"route": route, "gate_up": gate_up, "down": down}
 
@@ -508,7 +526,8 @@ def main():
         for p_ in (z, wn, xin):
             dev.free(p_)
 
-    sbytes = stage_bytes(shape)
+    # the one-token exact decode runs k_router / k_gu_dec / k_dn_dec for dm = 2048 layers
+    sbytes = stage_bytes(shape, shared_in_gu=(tier == em.EXACT and shape.dm == 2048))
     dom = max(("gate_up", "down"), key=lambda k: stages.get(k, (0, 0))[0])
     dom_us = stages[dom][0]
     ach = sbytes[dom] / (dom_us * 1e-6) / 1e9

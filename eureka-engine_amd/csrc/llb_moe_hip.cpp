@@ -173,6 +173,38 @@ int llb_hip_read(void* h, llb_dptr p, size_t bytes) {
 }
 int llb_hip_sync(void) { return hip_ok(hipStreamSynchronize(g_stream), "llb_sync"); }
 
+// kernel by name and LLB_LAUNCH (host/llb_backend.h:11-24; the CUDA twin's cuModuleGetFunction and
+// cuLaunchKernel, host/llb_backend_cuda.h:7-11,82-99): a code object loaded once, its kernels looked up
+// by name, launched gx * gy groups of bx threads with sm bytes of dynamic LDS on the library's stream,
+// each argument the address of a host variable holding its value (the values are copied at the call)
+int llb_hip_module_load(const char* path, uint64_t* module) {
+  if (!path || !module) return fail(LLB_HIP_EINVAL, "module_load: null argument");
+  hipModule_t m = nullptr;
+  int rc = hip_ok(hipModuleLoad(&m, path), "hipModuleLoad");
+  if (rc) return rc;
+  *module = (uint64_t)(uintptr_t)m;
+  return 0;
+}
+int llb_hip_module_function(uint64_t module, const char* name, void** fn) {
+  if (!module || !name || !fn) return fail(LLB_HIP_EINVAL, "module_function: null argument");
+  hipFunction_t f = nullptr;
+  int rc = hip_ok(hipModuleGetFunction(&f, (hipModule_t)(uintptr_t)module, name), "hipModuleGetFunction");
+  if (rc) return fail(rc, "module_function: no kernel named %s", name);
+  *fn = (void*)f;
+  return 0;
+}
+int llb_hip_launch(void* fn, uint32_t gx, uint32_t gy, uint32_t bx, uint32_t sm, void** args, uint32_t na) {
+  if (!fn) return fail(LLB_HIP_EINVAL, "launch: null kernel");
+  if (!gx || !gy || !bx || bx > 1024) return fail(LLB_HIP_EINVAL, "launch: grid %u x %u of %u threads", gx, gy, bx);
+  if (sm > 160 * 1024) return fail(LLB_HIP_EINVAL, "launch: %u bytes of LDS (at most 160 KiB)", sm);
+  if (na && !args) return fail(LLB_HIP_EINVAL, "launch: %u arguments but no argument array", na);
+  for (uint32_t i = 0; i < na; i++)
+    if (!args[i]) return fail(LLB_HIP_EINVAL, "launch: argument %u is a null address", i);
+  return hip_ok(hipModuleLaunchKernel((hipFunction_t)fn, gx, gy, 1, bx, 1, 1, sm, g_stream, na ? args : nullptr,
+                                      nullptr),
+                "hipModuleLaunchKernel");
+}
+
 // graph record / replay (llb_graph_begin / llb_graph_end, host/llb_backend_cuda.h:125-184): the
 // launches between begin and end are captured from the library's stream (a capture needs a
 // non-null stream: the library makes its own when none is set) and replayed as one graph

@@ -1,11 +1,16 @@
 /* moe_layer_drv.c -- a standalone C host for one MoE layer, in the role of llb_moe_run
- * (host/llb_host.c:622-724), over the C ABI only (include/llb_moe_hip.h).
+ * (host/llb_host.c:622-724), over the C ABI only: the backend contract of host/llb_backend.h through
+ * include/llb_backend_hip.h (LLB_LAUNCH, llb_alloc_zero, llb_read, llb_sync) and the layer entry points
+ * of include/llb_moe_hip.h.
  *
  * It lays out one layer's Bytes region the way a table row points into it: the shared expert's gate,
  * up and down matrices (words 3..5), the router rows (word 21) and the shared gate row (word 22). It
  * fills that region, the expert stacks and the inputs with the library's seeded generator (the same
  * streams as the Python test harness: stream = layer * 16 + tensor slot). It writes the 32 table
- * words (tools/gguf2pack.c:1142-1146) and runs the layer through llb_moe_run_table, which does the
+ * words (tools/gguf2pack.c:1142-1146). The generator writes the token rows into staging buffers; a
+ * kernel of drv_kernels.hsaco (next to this binary), looked up by name and launched with LLB_LAUNCH's
+ * argument-address convention (a by-value struct, a float), stages them into the layer's inputs. Then
+ * it runs the layer through llb_moe_run_table, which does the
  * admission check, the field decode and the forward. Then it writes y [T][dm], ids [T][nk] and
  * wt [T][nk] to a file and prints a one-line summary.
  *
@@ -16,8 +21,9 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
-#include "../../include/llb_moe_hip.h"
+#include "../../include/llb_backend_hip.h"
 
 enum { ST_ROUTER, ST_SHGATE, ST_G, ST_U, ST_D, ST_SG, ST_SU, ST_SD, ST_H2, ST_X1 };
 #define W_SIGMA 0.02f
@@ -42,7 +48,7 @@ static int ok(int rc, const char* what) {
   return rc;
 }
 static llb_dptr alloc(uint64_t n) {
-  llb_dptr p = llb_hip_alloc_zero((size_t)n);
+  llb_dptr p = llb_alloc_zero((size_t)n);
   if (!p) {
     fprintf(stderr, "moe_layer_drv: alloc of %llu bytes failed: %s\n", (unsigned long long)n, llb_hip_last_error());
     exit(1);
@@ -120,23 +126,48 @@ int main(int argc, char** argv) {
   const uint64_t n = (uint64_t)T * dm;
   const llb_dptr h2 = alloc(n * 4), x1 = alloc(n * 4), y = alloc(n * 4);
   const llb_dptr ids = alloc((uint64_t)T * nk * 4), wt = alloc((uint64_t)T * nk * 4);
-  ok(llb_moe_hip_gen_gauss(seed, ST_H2, 0, n, 1.0f, h2), "h2");
-  ok(llb_moe_hip_gen_gauss(seed, ST_X1, 0, n, 1.0f, x1), "x1");
+  const llb_dptr hs = alloc(n * 4), xs = alloc(n * 4);
+  ok(llb_moe_hip_gen_gauss(seed, ST_H2, 0, n, 1.0f, hs), "h2");
+  ok(llb_moe_hip_gen_gauss(seed, ST_X1, 0, n, 1.0f, xs), "x1");
+  /* the staging kernel, by name from the code object beside this binary */
+  char path[4096];
+  const ssize_t pl = readlink("/proc/self/exe", path, sizeof path - 32);
+  if (pl <= 0) return 1;
+  path[pl] = 0;
+  char* slash = strrchr(path, '/');
+  strcpy(slash ? slash + 1 : path, "drv_kernels.hsaco");
+  uint64_t mod = 0;
+  void* k_stage = NULL;
+  ok(llb_hip_module_load(path, &mod), "llb_hip_module_load");
+  ok(llb_hip_module_function(mod, "llb_drv_stage", &k_stage), "llb_hip_module_function");
+  struct {
+    llb_dptr src, dst;
+    uint32_t n, pad;
+  } sa = {hs, h2, (uint32_t)n, 0}, sb2 = {xs, x1, (uint32_t)n, 0};
+  float one = 1.0f;
+  if (!LLB_LAUNCH(k_stage, (n + 255) / 256, 2, 256, &sa, &sb2, &one)) {
+    fprintf(stderr, "moe_layer_drv: LLB_LAUNCH failed: %s\n", llb_hip_last_error());
+    return 1;
+  }
   llb_moe_layer L;
   ok(llb_moe_layer_from_table(w, dm, base, G, U, D, &L), "llb_moe_layer_from_table");
   const size_t sb = llb_moe_hip_scratch_bytes(&L, (uint32_t)T, tier);
   const llb_dptr scratch = alloc(sb);
   ok(llb_moe_run_table(w, dm, df, len, base, G, U, D, (uint32_t)T, h2, x1, y, ids, wt, scratch, sb, tier),
      "llb_moe_run_table");
-  ok(llb_hip_sync(), "llb_hip_sync");
+  if (!llb_sync()) {
+    fprintf(stderr, "moe_layer_drv: llb_sync failed: %s\n", llb_hip_last_error());
+    return 1;
+  }
 
   float* hy = (float*)malloc(n * 4);
   uint32_t* hid = (uint32_t*)malloc((size_t)T * nk * 4);
   float* hwt = (float*)malloc((size_t)T * nk * 4);
   if (!hy || !hid || !hwt) return 1;
-  ok(llb_hip_read(hy, y, n * 4), "read y");
-  ok(llb_hip_read(hid, ids, (size_t)T * nk * 4), "read ids");
-  ok(llb_hip_read(hwt, wt, (size_t)T * nk * 4), "read wt");
+  if (!llb_read(hy, y, n * 4) || !llb_read(hid, ids, (size_t)T * nk * 4) || !llb_read(hwt, wt, (size_t)T * nk * 4)) {
+    fprintf(stderr, "moe_layer_drv: llb_read failed: %s\n", llb_hip_last_error());
+    return 1;
+  }
   FILE* f = fopen(argv[5], "wb");
   if (!f || fwrite(hy, 4, n, f) != n || fwrite(hid, 4, (size_t)T * nk, f) != (size_t)T * nk ||
       fwrite(hwt, 4, (size_t)T * nk, f) != (size_t)T * nk || fclose(f) != 0) {

@@ -54,6 +54,14 @@ int llb_hip_write(llb_dptr d, const void* h, size_t bytes);    /* llb_write, llb
 int llb_hip_read(void* h, llb_dptr p, size_t bytes);           /* llb_read, llb_backend_cuda.h:198-201 */
 int llb_hip_sync(void);                                        /* llb_sync, llb_backend_cuda.h:216-219 */
 int llb_hip_mem_info(size_t* free_bytes, size_t* total_bytes); /* cuMemGetInfo, host/llb_host.c:531 */
+/* kernel by name (cuModuleGetFunction, host/llb_backend.h:37-39) and LLB_LAUNCH / LLB_LAUNCH_SM
+ * (host/llb_backend.h:11-24, host/llb_backend_cuda.h:7-11,82-99): load a gfx950 code object, look up a
+ * kernel, launch gx x gy groups of bx threads with sm bytes of dynamic LDS on the library's stream.
+ * args[i] is the address of a host variable holding argument i; na counts them. The C macros over these
+ * are in llb_backend_hip.h. */
+int llb_hip_module_load(const char* path, uint64_t* module);
+int llb_hip_module_function(uint64_t module, const char* name, void** fn);
+int llb_hip_launch(void* fn, uint32_t gx, uint32_t gy, uint32_t bx, uint32_t sm, void** args, uint32_t na);
 /* graph record / replay: llb_graph_begin / llb_graph_end (host/llb_backend_cuda.h:125-184). Launches
  * between begin and end are captured (not run); launch replays them on the library's stream.
  * No allocation, copy or read may happen inside a capture (the reference bails to eager there). */

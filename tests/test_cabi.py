@@ -16,6 +16,9 @@ def declared():
         if f.endswith(".h"):
             src = open(os.path.join(ROOT, "include", f)).read()
             src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+            # macros and header-only static inline wrappers (llb_backend_hip.h) are not library symbols
+            src = re.sub(r"#define(?:[^\n]*\\\n)*[^\n]*", "", src)
+            src = re.sub(r"static inline [^{]*\{[^}]*\}", "", src)
             names |= set(re.findall(r"\b(llb_\w+)\s*\(", src))
     return names
 
