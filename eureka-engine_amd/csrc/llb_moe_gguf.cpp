@@ -22,6 +22,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <new>
 #include <string>
 #include <thread>
 #include <vector>
@@ -336,10 +337,19 @@ struct StreamSrc {
   uint32_t* slots;      // device [nk] = 0 .. nk - 1: the ids the expert kernels see
   uint32_t nk;
 };
+static void free_stream(StreamSrc* s) {
+  if (!s) return;
+  (void)hipStreamSynchronize(llb_cur_stream());
+  (void)hipHostFree(s->pin);
+  (void)hipFree(s->dev);
+  (void)hipFree(s->slots);
+  munmap((void*)s->map, (size_t)s->map_bytes);
+  delete s;
+}
 
 extern "C" {
 
-int llb_moe_hip_load_layer(llb_gguf* g, uint32_t layer, int mode, llb_moe_layer* L) {
+static int load_layer_impl(llb_gguf* g, uint32_t layer, int mode, llb_moe_layer* L) {
   if (!g || !L) return llb_fail_msg(LLB_HIP_EINVAL, "load: null file or layer");
   if (mode < LLB_MOE_RES_DEVICE || mode > LLB_MOE_RES_STREAM) return llb_fail_msg(LLB_HIP_EINVAL, "load: no such mode");
   const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
@@ -420,7 +430,21 @@ int llb_moe_hip_load_layer(llb_gguf* g, uint32_t layer, int mode, llb_moe_layer*
   uint32_t own = 0;
   for (int i = 0; i < 5; i++)
     if (ot[i]) {
-      if ((rc = fill(g, *ot[i], LLB_MOE_RES_DEVICE, opt[i].dst, opt[i].nm))) return rc;
+      if ((rc = fill(g, *ot[i], LLB_MOE_RES_DEVICE, opt[i].dst, opt[i].nm))) {
+        // unwind: the optional tensors filled so far, then the stacks or the stream state
+        for (int k = 0; k < i; k++)
+          if (own >> k & 1) {
+            free_stack(LLB_MOE_RES_DEVICE, *opt[k].dst);
+            *opt[k].dst = 0;
+          }
+        if (mode == LLB_MOE_RES_STREAM) {
+          free_stream((StreamSrc*)(uintptr_t)L->stream);
+          L->stream = 0;
+        } else {
+          for (int k = 0; k < 3; k++) free_stack(mode, got[k]);
+        }
+        return rc;
+      }
       own |= 1u << i;
     }
   L->G = got[0];
@@ -428,6 +452,83 @@ int llb_moe_hip_load_layer(llb_gguf* g, uint32_t layer, int mode, llb_moe_layer*
   L->D = got[2];
   L->res = (uint32_t)mode;
   L->own = own;
+  return 0;
+}
+int llb_moe_hip_load_layer(llb_gguf* g, uint32_t layer, int mode, llb_moe_layer* L) {
+  try {
+    return load_layer_impl(g, layer, mode, L);
+  } catch (...) {  // a bad_alloc of the stream state: nothing crosses the C ABI
+    return llb_fail_msg(LLB_HIP_EDEVICE, "load: out of host memory");
+  }
+}
+
+// llb_moe_load's residency choice (host/llb_host.c:532-545): the routed experts' bytes over the n layers
+// (each stack checked against the file as load_layer checks it), against free device memory less a
+// 0.75 GiB reserve (device), then MemAvailable less 4 GiB (host), else stream. LLB_MOE_VRAM / LLB_MOE_RAM
+// (bytes) stand in for the two capacities, LLB_MOE_EXPERTS=device|host|stream forces the mode; one line
+// on stderr names the choice and its inputs.
+static uint64_t env_bytes(const char* k, bool* set) {
+  const char* e = getenv(k);
+  *set = e && *e;
+  return *set ? strtoull(e, nullptr, 10) : 0;
+}
+static uint64_t mem_available() {
+  FILE* f = fopen("/proc/meminfo", "r");
+  if (!f) return 0;
+  char ln[256];
+  uint64_t kb = 0;
+  while (fgets(ln, sizeof ln, f))
+    if (!strncmp(ln, "MemAvailable:", 13)) kb = strtoull(ln + 13, nullptr, 10);
+  fclose(f);
+  return kb * 1024;
+}
+int llb_moe_hip_residency(const llb_gguf* g, const uint32_t* layers, const llb_moe_layer* L, uint32_t n, int* mode,
+                          uint64_t* expert_bytes) {
+  if (!g || !layers || !L || !mode || !n) return llb_fail_msg(LLB_HIP_EINVAL, "residency: null argument or no layers");
+  uint64_t tot = 0;
+  int rc = 0;
+  for (uint32_t i = 0; i < n; i++) {
+    const llb_moe_layer& l = L[i];
+    const uint32_t fg = l.fx & 15, fu = l.fx >> 4 & 15, fd = l.fx >> 8 & 15, fz = l.fx >> 12 & 1;
+    const uint64_t rbg = row_bytes(fg, l.dm), rbu = row_bytes(fu, l.dm), rbd = row_bytes(fd, l.ef);
+    if (!l.dm || !l.ne || !l.ef || !rbg || !rbu || !rbd)
+      return llb_fail_msg(LLB_HIP_EINVAL, "residency: a layer's shape words are not set");
+    const GgTensor* t = want(g, layers[i], fz ? "ffn_gate_up_exps" : "ffn_gate_exps", fg,
+                             (uint64_t)l.ne * (fz ? 2 : 1) * l.ef * rbg, &rc);
+    if (!t) return rc;
+    tot += t->bytes;
+    if (!fz) {
+      if (!(t = want(g, layers[i], "ffn_up_exps", fu, (uint64_t)l.ne * l.ef * rbu, &rc))) return rc;
+      tot += t->bytes;
+    }
+    if (!(t = want(g, layers[i], "ffn_down_exps", fd, (uint64_t)l.ne * l.dm * rbd, &rc))) return rc;
+    tot += t->bytes;
+  }
+  bool vset, rset;
+  uint64_t vram = env_bytes("LLB_MOE_VRAM", &vset), ram = env_bytes("LLB_MOE_RAM", &rset);
+  if (!vset) {
+    size_t fr = 0, tv = 0;
+    if (hipMemGetInfo(&fr, &tv) != hipSuccess) {
+      (void)hipGetLastError();
+      return llb_fail_msg(LLB_HIP_EDEVICE, "residency: hipMemGetInfo failed (set LLB_MOE_VRAM to choose without a device)");
+    }
+    vram = fr;
+  }
+  if (!rset) ram = mem_available();
+  const uint64_t rv = 3ull << 28, rr = 4ull << 30;
+  const char* e = getenv("LLB_MOE_EXPERTS");
+  int m;
+  if (e && !strcmp(e, "device")) m = LLB_MOE_RES_DEVICE;
+  else if (e && !strcmp(e, "host")) m = LLB_MOE_RES_HOST;
+  else if (e && !strcmp(e, "stream")) m = LLB_MOE_RES_STREAM;
+  else m = tot + rv <= vram ? LLB_MOE_RES_DEVICE : tot + rr <= ram ? LLB_MOE_RES_HOST : LLB_MOE_RES_STREAM;
+  static const char* mn[3] = {"device (VRAM)", "host (pinned, device-mapped RAM)",
+                              "stream (mmapped GGUF, the k experts copied per token)"};
+  fprintf(stderr, "moe: %u layers, experts %.2f GiB -> %s [free VRAM %.2f GiB%s, MemAvailable %.2f GiB%s]\n", n,
+          tot / 1073741824.0, mn[m], vram / 1073741824.0, vset ? " (LLB_MOE_VRAM)" : "", ram / 1073741824.0,
+          rset ? " (LLB_MOE_RAM)" : "");
+  *mode = m;
+  if (expert_bytes) *expert_bytes = tot;
   return 0;
 }
 
@@ -493,17 +594,39 @@ struct GatherPool {
 };
 // the pool of this process: a child made by fork() inherits the pool's memory but not its threads, so
 // a pool made by another process id is left behind (never touched again) and a new one is made
+// A pool that cannot be made (no memory, a thread limit) is not an error: the caller copies on its own
+// thread instead, and this process does not try again. No exception leaves this function, so none reaches
+// the C entry points above it.
 GatherPool* gather_pool() {
   static std::mutex mk;
   static GatherPool* p = nullptr;
   static pid_t owner = 0;
+  static bool broken = false;
   std::lock_guard<std::mutex> lk(mk);
   if (!p || owner != getpid()) {
-    p = new GatherPool;  // never freed: detached workers wait on it until the process ends
+    if (broken && owner == getpid()) return nullptr;
     owner = getpid();
-    for (unsigned i = 1; i < kGather; i++) std::thread(&GatherPool::worker, p, i).detach();
+    p = new (std::nothrow) GatherPool;  // never freed: detached workers wait on it until the process ends
+    unsigned made = 1;
+    if (p) {
+      try {
+        for (; made < kGather; made++) std::thread(&GatherPool::worker, p, made).detach();
+      } catch (...) {
+      }
+    }
+    if (!p || made < kGather) {  // the workers made so far keep waiting on the abandoned pool
+      p = nullptr;
+      broken = true;
+    }
   }
   return p;
+}
+// the same job on the calling thread
+void gather_here(uint8_t* dst, const std::vector<Seg>& sv) {
+  for (const Seg& g : sv) {
+    memcpy(dst, g.src, g.len);
+    dst += g.len;
+  }
 }
 }  // namespace
 
@@ -511,7 +634,7 @@ GatherPool* gather_pool() {
 // host/llb_host.c:680-696): ids read back, the experts' gate (+ up) and down bytes gathered from the
 // mapped file into pinned memory by the pool, then uploaded on the library stream. The slot ids 0..k-1
 // replace the experts' ids for the expert kernels.
-int stream_stage(const llb_moe_layer* L, const uint32_t* d_ids, const uint32_t** slots) {
+static int stream_stage_impl(const llb_moe_layer* L, const uint32_t* d_ids, const uint32_t** slots) {
   auto* s = (StreamSrc*)(uintptr_t)L->stream;
   if (!s) return llb_fail_msg(LLB_HIP_EINVAL, "stream: the layer has no stream source");
   const hipStream_t st = llb_cur_stream();
@@ -535,13 +658,22 @@ int stream_stage(const llb_moe_layer* L, const uint32_t* d_ids, const uint32_t**
     if (!len[k]) continue;  // fused stacks: the up rows travel with the gate rows
     sv.clear();
     for (uint32_t j = 0; j < s->nk; j++) sv.push_back({s->map + base[k] + ids[j] * es[k], len[k]});
-    pool->run(pin + at, sv);
+    if (pool) pool->run(pin + at, sv);
+    else gather_here(pin + at, sv);
     if (hipMemcpyAsync(dev + at, pin + at, s->nk * len[k], hipMemcpyHostToDevice, st) != hipSuccess)
       return llb_fail_msg(LLB_HIP_EDEVICE, "stream: cannot stage the experts");
     at += s->nk * len[k];
   }
   *slots = s->slots;
   return 0;
+}
+// no exception (a vector's bad_alloc) crosses into the C entry point that calls this
+int stream_stage(const llb_moe_layer* L, const uint32_t* d_ids, const uint32_t** slots) {
+  try {
+    return stream_stage_impl(L, d_ids, slots);
+  } catch (...) {
+    return llb_fail_msg(LLB_HIP_EDEVICE, "stream: out of host memory staging the experts");
+  }
 }
 // the pinned staging is reused by the next token: wait for this token's uploads (the caller, after
 // the expert kernels are queued)
@@ -552,15 +684,7 @@ int stream_done() {
 extern "C" int llb_moe_hip_unload_layer(llb_moe_layer* L) {
   if (!L) return llb_fail_msg(LLB_HIP_EINVAL, "unload: null layer");
   if (L->res == LLB_MOE_RES_STREAM) {
-    auto* s = (StreamSrc*)(uintptr_t)L->stream;
-    if (s) {
-      (void)hipStreamSynchronize(llb_cur_stream());
-      (void)hipHostFree(s->pin);
-      (void)hipFree(s->dev);
-      (void)hipFree(s->slots);
-      munmap((void*)s->map, (size_t)s->map_bytes);
-      delete s;
-    }
+    free_stream((StreamSrc*)(uintptr_t)L->stream);
     L->stream = 0;
   } else {
     free_stack((int)L->res, L->G);

@@ -162,6 +162,15 @@ int llb_gguf_tensor_at(const llb_gguf* g, uint64_t i, char* name, size_t cap, ui
                        uint32_t* type, uint32_t* nd, uint64_t* dims);
 int llb_moe_hip_load_layer(llb_gguf* g, uint32_t layer, int mode, llb_moe_layer* L);
 int llb_moe_hip_unload_layer(llb_moe_layer* L);
+/* llb_moe_load's residency choice (host/llb_host.c:532-545): sums the routed stacks of the n layers
+ * (layers[i] is L[i]'s block index; each stack checked as load_layer checks it) and picks DEVICE when they
+ * fit free device memory less 0.75 GiB, else HOST when they fit MemAvailable less 4 GiB, else STREAM.
+ * Environment: LLB_MOE_VRAM / LLB_MOE_RAM (bytes) replace the two capacities (with LLB_MOE_VRAM set no
+ * device is queried); LLB_MOE_EXPERTS=device|host|stream forces the mode. Prints the reference's
+ * "moe: N layers, experts X GiB -> mode [free VRAM .., MemAvailable ..]" line on stderr. expert_bytes
+ * may be null. */
+int llb_moe_hip_residency(const llb_gguf* g, const uint32_t* layers, const llb_moe_layer* L, uint32_t n, int* mode,
+                          uint64_t* expert_bytes);
 
 /* ---- packed weights for the f16 tier. No counterpart in the reference, whose prefill decodes GGUF
  * blocks where they lie. The grouped GEMM reads each weight tile of 32 rows x 64 columns as one
