@@ -516,13 +516,20 @@ int mo_moe_exact(const mo_layer* L, u32 T, const float* h2, const float* x1, flo
 /* pf_q8x (tools/pf27/pfmm.cuh:39-54) / ref_q8x (tools/q4dp/q4dp_ref.h:18-30) */
 void mo_q8_1(const float* x, u32 n, int8_t* q, float* d, float* s) {
   for (u32 b = 0; b < n / 32; b++) {
-    float a = 0.0f, sm = 0.0f;
-    for (u32 i = 0; i < 32; i++) { a = fmaxf(a, fabsf(x[32 * b + i])); sm = sm + x[32 * b + i]; }
+    /* the block's sum in pf_q8x's warp order: lane l adds lane l ^ m's value, m = 16, 8, 4, 2, 1;
+     * lane 0's total is stored */
+    float a = 0.0f, v[32];
+    for (u32 i = 0; i < 32; i++) { a = fmaxf(a, fabsf(x[32 * b + i])); v[i] = x[32 * b + i]; }
+    for (u32 m = 16; m > 0; m >>= 1) {
+      float t[32];
+      for (u32 l = 0; l < 32; l++) t[l] = v[l] + v[l ^ m];
+      memcpy(v, t, sizeof v);
+    }
     const float dd = a / 127.0f;
     for (u32 i = 0; i < 32; i++)
       q[32 * b + i] = a == 0.0f ? 0 : (int8_t)clampi((int)roundf(x[32 * b + i] / dd), -127, 127);
     d[b] = dd;
-    s[b] = sm;
+    s[b] = v[0];
   }
 }
 

@@ -11,6 +11,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE = os.path.join(ROOT, "oracle", "libmoe_oracle.so")
 REF = os.path.join(ROOT, "oracle", "_ref", "libref_q35.so")
+REF_Q4DP = os.path.join(ROOT, "oracle", "_ref", "libref_q4dp.so")
 
 F32, Q8_0, Q4_K, Q6_K, Q5_K = 0, 1, 3, 4, 9
 BLOCK = {F32: (4, 1), Q8_0: (34, 32), Q4_K: (144, 256), Q6_K: (210, 256), Q5_K: (176, 256)}
@@ -74,6 +75,18 @@ def lib():
             f = getattr(_lib, n)
             f.restype, f.argtypes = r, a
     return _lib
+
+
+def ref_q4dp():
+    """The reference's q8 CPU twin, tools/q4dp/q4dp_ref.h, compiled by oracle/Makefile (None if not built)."""
+    if not os.path.exists(REF_Q4DP):
+        return None
+    r = C.CDLL(REF_Q4DP)
+    r.ref_q8x_c.restype, r.ref_q8x_c.argtypes = None, [P, P, P, C.c_uint32]
+    r.ref_sb_c.restype = C.c_float
+    r.ref_sb_c.argtypes = [P, P, P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_int]
+    r.ref_row_c.restype, r.ref_row_c.argtypes = C.c_float, [P, C.c_uint32, P, P, C.c_uint32, C.c_int]
+    return r
 
 
 def ref_lib():

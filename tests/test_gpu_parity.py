@@ -329,7 +329,7 @@ def test_q8_1_matches_oracle(dev):
     ol.lib().mo_q8_1(ol.ptr(x), 4096, ol.ptr(rq), ol.ptr(rd), ol.ptr(rs))
     assert np.array_equal(gq, rq)
     assert np.array_equal(gds[:, 0], rd)
-    assert np.allclose(gds[:, 1], rs, rtol=1e-5, atol=1e-5)
+    assert np.array_equal(gds[:, 1], rs)  # s: the same xor-butterfly order
 
 
 @pytest.mark.parametrize("name,T", [("c2", 1), ("c1", 4), ("c2", 8), ("c1", 16)])

@@ -324,3 +324,186 @@ def test_oracle_threads_give_the_same_bits():
     y1, _, _, _ = hl.run(h2, None, nthreads=1)
     y4, _, _, _ = hl.run(h2, None, nthreads=4)
     assert np.array_equal(bits(y1), bits(y4))
+
+
+def _exp_hit(k):
+    """a float x whose exp through F64, rounded to float, is exactly 2^-k (the oracle's exp is
+    (float)exp((double)x), pinned against the reference's hf_exp above)"""
+    x0 = np.float32(-k * np.log(2))
+    for d in range(200):
+        for s in (1, -1):
+            x = x0
+            for _ in range(d):
+                x = np.nextafter(x, np.float32(100 * s))
+            if np.float32(np.exp(np.float64(x))) == np.float32(2.0 ** -k):
+                return x
+    raise AssertionError(k)
+
+
+def test_topk_softmax_sum_order_known_answer():
+    """llb_moe_topk's sum (tools/payload-moeany.patch:346-371): thread t of 1024 adds p[e], e = t mod 1024,
+    in ascending e; each warp of 32 folds by xor 16, 8, 4, 2, 1 (own value first); thread 0 adds the 32
+    warp sums in order from 0. The case below has only powers of two, so each partial sum can be followed
+    by hand, and the 1024-thread order gives a different total from a sequential sum and from a 256-thread
+    block, and through it different weights.
+
+    ne = 16384. p = 1 at e = l + 256 j (l < 32, j < 32: 1024 ones), p = 2^-14 at e = 8224 and 8256,
+    p = 1/2 at e = 10241, p = 0 elsewhere (logit -inf).
+      sequential: the ones end at e = 7967 with 1024; each 2^-14 then is half an ulp of 1024 and ties to
+        even (1024); + 1/2 -> 1024.5.
+      256 threads: warp 0 (e mod 256 < 32) holds every one and the 1/2: 1024.5; warps 1 and 2 hold one
+        2^-14 each, and each ties away at 1024.5 (its last mantissa bit is even) -> 1024.5.
+      1024 threads: thread l + 256 q holds 8 ones; warps 0, 8, 16, 24 sum 256 (warp 0 256.5); warps 1
+        and 2 hold the two 2^-14 and meet the total while it is 256.5 (ulp 2^-15): exact. The total runs
+        256.5, +2^-14, +2^-14, 512.5 + 2^-13, 768.5 + 2^-13, 1024.5 + 2^-13: exact throughout.
+    With k = 3 (ids 0, 1, 2, all p = 1) the weights are inv / (3 inv), inv = 1 / total, renormalised: the
+    two totals give different bits."""
+    ne, nk = 16384, 3
+    lg = np.full(ne, -np.inf, np.float32)
+    for l in range(32):
+        lg[l + 256 * np.arange(32)] = 0.0
+    lg[[8224, 8256]] = _exp_hit(14)
+    lg[1 + 256 * 40] = _exp_hit(1)
+    ids, wt, _ = _topk(lg, nk)
+    assert list(ids) == [0, 1, 2]
+
+    def weights(total):
+        inv = np.float32(1.0) / np.float32(total)
+        s = np.float32(np.float32(inv + inv) + inv)
+        return np.full(nk, inv / s, np.float32)
+
+    want = weights(1024.5 + 2.0 ** -13)
+    other = weights(1024.5)  # the sequential and the 256-thread totals
+    assert not np.array_equal(want.view(np.uint32), other.view(np.uint32))
+    assert np.array_equal(wt.view(np.uint32), want.view(np.uint32))
+
+
+def _q4dp():
+    r = ol.ref_q4dp()
+    if r is None:
+        pytest.skip("oracle/_ref/libref_q4dp.so is not built (make -C oracle ref; needs the reference tree)")
+    return r
+
+
+def _q8_1(x):
+    n = x.size
+    q, d, s = np.zeros(n, np.int8), np.zeros(n // 32, np.float32), np.zeros(n // 32, np.float32)
+    lib.mo_q8_1(ol.ptr(x), n, ol.ptr(q), ol.ptr(d), ol.ptr(s))
+    return q, d, s
+
+
+def test_q8_1_matches_the_reference_twin():
+    """q and d bit for bit against ref_q8x (tools/q4dp/q4dp_ref.h:18-30) on finite blocks: normal, zero,
+    tiny (subnormal d), huge, one-hot, and halfway values that roundf takes away from zero. (For a block
+    holding inf / NaN the twin stores d = NaN and q = 0; pf_q8x, which the oracle follows, has no such
+    branch: such inputs are outside the path's envelope.)"""
+    r = _q4dp()
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal(32 * 64).astype(np.float32)
+    xb = x.reshape(64, 32)
+    xb[1] = 0.0
+    xb[2] *= np.float32(1e-38)
+    xb[3] *= np.float32(1e36)
+    xb[4] = 0.0
+    xb[4, 7] = -3.0
+    xb[5] = (np.arange(32, dtype=np.float32) - 16.0) + 0.5  # amax 16.5: x / d lands near halves
+    xb[6] = np.float32(127.0) * (np.arange(32) % 3 - 1).astype(np.float32) / np.float32(2.0)
+    q, d, _ = _q8_1(x)
+    rq, rd = np.zeros(x.size, np.int8), np.zeros(64, np.float32)
+    r.ref_q8x_c(ol.ptr(x), ol.ptr(rq), ol.ptr(rd), x.size)
+    assert np.array_equal(q, rq)
+    assert np.array_equal(d.view(np.uint32), rd.view(np.uint32))
+
+
+def test_q8_1_sum_is_the_warp_butterfly():
+    """s is pf_q8x's xor-butterfly sum (tools/pf27/pfmm.cuh:44-48), lane 0's value. x0 = 2^24, x1 = x3 =
+    1: the butterfly meets x1 + x3 = 2 (level 2) before 2^24 (level 1): 2^24 + 2, exact. A sequential
+    sum loses each 1 against 2^24: 2^24."""
+    x = np.zeros(32, np.float32)
+    x[0], x[1], x[3] = BIG, 1.0, 1.0
+    _, _, s = _q8_1(x)
+    assert s[0] == BIG + 2
+
+
+def _q4k_exact_case(rng, nsb):
+    """a Q4_K row and q8_1 activations on which every product and sum of the block dot is exact in f32:
+    d = 2^-8, dmin = 2^-9, each 32-block of x is q dx with |q| <= 3 but one +-127, dx = 2^-6 or 2^-7
+    (so d = amax / 127 = dx exactly and x / d = q), scales and nibbles random."""
+    row = bytearray()
+    for _ in range(nsb):
+        row += (0x1C00).to_bytes(2, "little") + (0x1800).to_bytes(2, "little")
+        row += bytes(rng.integers(0, 256, 12, dtype=np.uint8)) + bytes(rng.integers(0, 256, 128, dtype=np.uint8))
+    cols = 256 * nsb
+    q = rng.integers(-3, 4, cols).astype(np.int8).reshape(-1, 32)
+    q[np.arange(q.shape[0]), rng.integers(0, 32, q.shape[0])] = np.where(rng.random(q.shape[0]) < 0.5, 127, -127)
+    dx = np.where(rng.random(q.shape[0]) < 0.5, 2.0 ** -6, 2.0 ** -7).astype(np.float32)
+    x = (q.astype(np.float32) * dx[:, None]).ravel()
+    return np.frombuffer(bytes(row), np.uint8).copy(), x
+
+
+def _q4k_f64(row, x, nsb):
+    """the block dot in float64 from the format's definition (d sc q - dmin m per weight, times x)"""
+    w = np.zeros(256 * nsb, np.float32)
+    lib.mo_deq_row(em.Q4_K, ol.ptr(row), 256 * nsb, ol.ptr(w))
+    return float(np.dot(w.astype(np.float64), x.astype(np.float64)))
+
+
+@pytest.mark.parametrize("nsb", [1, 4])
+def test_q4k_block_dot_matches_the_reference_twin_and_its_mutants_fail(nsb):
+    """mo_dot_q8's Q4_K block dot (mx_blk, host/llb_pf.cuh:468-515) against the reference's twin ref_row /
+    ref_sb (tools/q4dp/q4dp_ref.h:32-74), bit for bit, on rows where all arithmetic is exact (so the two
+    summation orders and s = sum x against dx sum q cannot differ), and against float64 from the
+    dequantised row. The twin's own mutation controls (mut 1: a scale + 1, 2: nibbles swapped, 3: x one
+    block off, 4: the dmin term's sign) must each give another value."""
+    r = _q4dp()
+    rng = np.random.default_rng(40 + nsb)
+    for _ in range(8):
+        row, x = _q4k_exact_case(rng, nsb)
+        cols = 256 * nsb
+        q, d, s = _q8_1(x)
+        assert np.array_equal(q.astype(np.float32) * np.repeat(d, 32), x)  # the q8_1 is exact
+        ours = lib.mo_dot_q8(em.Q4_K, ol.ptr(row), cols, ol.ptr(q), ol.ptr(d), ol.ptr(s))
+        theirs = r.ref_row_c(ol.ptr(row), nsb, ol.ptr(q), ol.ptr(d), cols, 0)
+        exact = _q4k_f64(row, x, nsb)
+        assert ours == theirs == exact
+        shares = sum(float(r.ref_sb_c(ol.ptr(row[144 * sb:]), ol.ptr(q), ol.ptr(d), cols, sb, g, k, 0))
+                     for sb in range(nsb) for g in range(4) for k in range(4))
+        assert shares == exact
+        for mut in (1, 2, 3, 4):
+            assert r.ref_row_c(ol.ptr(row), nsb, ol.ptr(q), ol.ptr(d), cols, mut) != ours, mut
+
+
+def _exact_row(rng, fm, cols):
+    """a row of format fm whose every block dot against exact q8_1 activations is exact in f32: f16 scales
+    2^-8 / 2^-9 and 6-bit or int8 sub-scales kept small; the quant bits random"""
+    nb = cols // 256
+    out = bytearray()
+    if fm == em.Q8_0:
+        for _ in range(cols // 32):
+            out += (0x1C00).to_bytes(2, "little") + bytes(rng.integers(0, 256, 32, dtype=np.uint8))
+    elif fm == em.Q6_K:
+        for _ in range(nb):
+            sc = rng.integers(-15, 16, 16).astype(np.int8).tobytes()
+            out += bytes(rng.integers(0, 256, 192, dtype=np.uint8)) + sc + (0x1C00).to_bytes(2, "little")
+    else:  # Q4_K / Q5_K: d, dmin, 12 scale bytes, (Q5_K: 32 high-bit bytes), 128 nibble bytes
+        for _ in range(nb):
+            out += (0x1C00).to_bytes(2, "little") + (0x1800).to_bytes(2, "little")
+            out += bytes(rng.integers(0, 256, 12 + (32 if fm == em.Q5_K else 0) + 128, dtype=np.uint8))
+    return np.frombuffer(bytes(out), np.uint8).copy()
+
+
+@pytest.mark.parametrize("fm", [em.Q8_0, em.Q4_K, em.Q5_K, em.Q6_K])
+def test_q8_block_dots_exact_against_float64(fm):
+    """every format's q8 block dot (mx_blk, host/llb_pf.cuh:468-515) equals float64 of the dequantised row
+    (the decoders pinned against the reference build above) times x, on inputs where f32 is exact: a
+    dropped term, a wrong nibble, scale or sign changes the value"""
+    rng = np.random.default_rng(int(fm) + 70)
+    cols = 512
+    for _ in range(8):
+        row = _exact_row(rng, fm, cols)
+        _, x = _q4k_exact_case(rng, cols // 256)
+        q, d, s = _q8_1(x)
+        w = np.zeros(cols, np.float32)
+        lib.mo_deq_row(fm, ol.ptr(row), cols, ol.ptr(w))
+        exact = float(np.dot(w.astype(np.float64), x.astype(np.float64)))
+        assert lib.mo_dot_q8(fm, ol.ptr(row), cols, ol.ptr(q), ol.ptr(d), ol.ptr(s)) == exact
