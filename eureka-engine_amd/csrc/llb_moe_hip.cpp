@@ -294,7 +294,7 @@ static ExactScratch exact_layout(const llb_moe_layer* L, uint32_t T) {
 }
 
 struct GemmScratch {
-  size_t x16, off, xmap, inv, act, out, sact, shd, total;
+  size_t x16, off, xmap, inv, act, out, spill, sact, shd, total;
 };
 static GemmScratch gemm_layout(const llb_moe_layer* L, uint32_t T) {
   GemmScratch g;
@@ -306,6 +306,7 @@ static GemmScratch gemm_layout(const llb_moe_layer* L, uint32_t T) {
   g.inv = o; o += al(n * 4);
   g.act = o; o += al(n * L->ef * 2);
   g.out = o; o += al(n * L->dm * 2);
+  g.spill = o; o += al(n * L->dm * 4);  // f32 down outputs past f16's range (touched only there)
   g.sact = o; o += al((size_t)T * L->sf * 2 + 4);
   g.shd = o; o += al((size_t)T * L->dm * 4);
   g.total = o;
@@ -507,6 +508,7 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
   d.xmap = nullptr;
   d.out = gb + gs.out;
   d.o16 = 1;
+  d.spill = (float*)(gb + gs.spill);
   d.P0 = L->PD ? dp<uint8_t>(L->PD) : nullptr;
   d.P1 = nullptr;
   d.pes = pack_bytes(fd, L->dm, L->ef);
@@ -514,7 +516,7 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
   if ((rc = launched(launch_moe_gemm(d, fd, 1, maxt, g_stream), "expert down GEMM"))) return rc;
   stage_end(ST_DN);
   if (side && (rc = hip_ok(hipStreamWaitEvent(g_stream, side->join, 0), "join hipStreamWaitEvent"))) return rc;
-  return launched(launch_combine((const _Float16*)(gb + gs.out), inv, wt, L->nk, shd, (const float*)(sc + s.sgo), x1, y,
+  return launched(launch_combine((const _Float16*)(gb + gs.out), (const float*)(gb + gs.spill), inv, wt, L->nk, shd, (const float*)(sc + s.sgo), x1, y,
                                  L->dm, T, g_stream),
                   "combine");
 }

@@ -355,8 +355,15 @@ DEV void gemm3_body(const GemmArgs& g, _Float16* lds, u32 e, u32 base, u32 m0, u
 #pragma unroll
         for (u32 b = 0; b < 2; b++) {
           const u64 o = s * g.N + ntile * 256 + 64 * w + 32 * b + lr;
-          if (g.o16) ((_Float16*)g.out)[o] = (_Float16)acc[mf][b][i];
-          else ((float*)g.out)[o] = acc[mf][b][i];
+          if (g.o16) {
+            // an output past f16's range keeps its f32 value in the spill, which the combine reads
+            // wherever the f16 holds +-inf
+            const _Float16 hv = (_Float16)acc[mf][b][i];
+            ((_Float16*)g.out)[o] = hv;
+            if (__builtin_isinf((float)hv)) g.spill[o] = acc[mf][b][i];
+          } else {
+            ((float*)g.out)[o] = acc[mf][b][i];
+          }
         }
       }
     }
@@ -454,7 +461,8 @@ __global__ void __launch_bounds__(256, g3_blocks(F, MODE, PKD)) k_moe_gemm3(Gemm
 
 // y[t][r] = (sum_j, rank order, wt[t][j] out[inv[t nk + j]][r]) + sgo[t] shd[t][r] + x1[t][r]; the slots'
 // down outputs in f16 (half the bytes of the largest intermediate), their weighted sum in f32
-__global__ void __launch_bounds__(256) k_combine(const _Float16* __restrict__ out, const u32* __restrict__ inv,
+__global__ void __launch_bounds__(256) k_combine(const _Float16* __restrict__ out, const float* __restrict__ spill,
+                                                 const u32* __restrict__ inv,
                                                  const float* __restrict__ wt, u32 nk, const float* __restrict__ shd,
                                                  const float* __restrict__ sgo, const float* __restrict__ x1,
                                                  float* __restrict__ y, u32 dm) {
@@ -476,8 +484,13 @@ __global__ void __launch_bounds__(256) k_combine(const _Float16* __restrict__ ou
     for (u32 j = 0; j < 8; j++)
       if (j0 + j < nk) {
         typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-        const h4 hv = *(const h4*)(out + (u64)srow[j0 + j] * dm + r);
+        const u64 so = (u64)srow[j0 + j] * dm + r;
+        const h4 hv = *(const h4*)(out + so);
         v[j] = make_float4((float)hv[0], (float)hv[1], (float)hv[2], (float)hv[3]);
+        if (__builtin_isinf(v[j].x)) v[j].x = spill[so];
+        if (__builtin_isinf(v[j].y)) v[j].y = spill[so + 1];
+        if (__builtin_isinf(v[j].z)) v[j].z = spill[so + 2];
+        if (__builtin_isinf(v[j].w)) v[j].w = spill[so + 3];
       }
 #pragma unroll
     for (u32 j = 0; j < 8; j++) {
@@ -553,10 +566,11 @@ int launch_pack(u32 fm, const u8* W, u64 es, u64 rb, u32 R, u32 K, u32 ne, u8* P
   return -1;
 }
 
-int launch_combine(const _Float16* out, const u32* inv, const float* wt, u32 nk, const float* shd, const float* sgo,
-                   const float* x1, float* y, u32 dm, u32 T, hipStream_t st) {
-  if (dm % 4 || nk > 64) return -1;
-  hipLaunchKernelGGL(k_combine, dim3((dm / 4 + 255) / 256, T), dim3(256), 0, st, out, inv, wt, nk, shd, sgo, x1, y, dm);
+int launch_combine(const _Float16* out, const float* spill, const u32* inv, const float* wt, u32 nk, const float* shd,
+                   const float* sgo, const float* x1, float* y, u32 dm, u32 T, hipStream_t st) {
+  if (dm % 4 || nk > 64 || !spill) return -1;
+  hipLaunchKernelGGL(k_combine, dim3((dm / 4 + 255) / 256, T), dim3(256), 0, st, out, spill, inv, wt, nk, shd, sgo, x1,
+                     y, dm);
   return 0;
 }
 u32 gemm_bm() { return GM_BM; }

@@ -179,6 +179,7 @@ struct GemmArgs {
   uint32_t ne;            // experts (<= 1024) when off is set
   void* out;          // mode 0: f16 [slots][N]; mode 1: f32 [slots][N], or f16 with o16
   uint32_t o16;       // mode 1: f16 outputs
+  float* spill;       // o16: f32 [slots][N], written only where the f16 output is +-inf (|v| past 65504)
   const uint8_t* P0;  // packed W0 (null: read the GGUF rows)
   const uint8_t* P1;  // packed W1 (mode 0)
   uint64_t pes;       // packed expert stride
@@ -194,7 +195,7 @@ int launch_rmsnorm_add(const float* x, const float* z, const float* w, float eps
 uint64_t pack_bytes(uint32_t fm, uint32_t R, uint32_t K);
 int launch_pack(uint32_t fm, const uint8_t* W, uint64_t es, uint64_t rb, uint32_t R, uint32_t K, uint32_t ne,
                 uint8_t* P, hipStream_t st);
-int launch_combine(const _Float16* out, const uint32_t* inv, const float* wt, uint32_t nk, const float* shd,
+int launch_combine(const _Float16* out, const float* spill, const uint32_t* inv, const float* wt, uint32_t nk, const float* shd,
                    const float* sgo, const float* x1, float* y, uint32_t dm, uint32_t T, hipStream_t st);
 int launch_exp(const float* x, float* y, uint64_t n, hipStream_t st);
 int launch_dequant(uint32_t fm, const uint8_t* W, uint64_t rb, uint32_t rows, uint32_t cols, float* out,

@@ -5,6 +5,8 @@ cos >= 0.9999) against the oracle's q8 mode. Dequant and the generator: bit-exac
 """
 import ctypes as C
 
+import os
+
 import numpy as np
 import pytest
 
@@ -513,10 +515,30 @@ def test_dequant_every_f16_scale(dev):
     dev.free(out)
 
 
-def _f16_case(dev, name, T, seed, sample=None):
+def _sample_tokens(ids, T, seed, n=64):
+    """n tokens to check against the oracle: the first 16 and the last 16 tokens routed to the expert with
+    the most slots (the first and last 64-slot tiles of its GEMM: slots are ordered by token within an
+    expert), token 0 and T - 1, then random others"""
+    flat = ids.ravel()
+    big = int(np.bincount(flat, minlength=int(flat.max()) + 1).argmax())
+    mine = np.nonzero((ids == big).any(axis=1))[0]
+    pick = list(dict.fromkeys([0, T - 1] + mine[:16].tolist() + mine[-16:].tolist()))
+    rest = np.random.default_rng(seed).permutation(T)
+    for t in rest:
+        if len(pick) >= min(n, T):
+            break
+        if int(t) not in pick:
+            pick.append(int(t))
+    return np.array(sorted(pick)), big, mine
+
+
+ORACLE_THREADS = min(16, os.cpu_count() or 1)
+
+
+def _f16_case(dev, name, T, seed, sample=None, bias=None):
     shape = em.SHAPES[name]
     _say("f16 tier", name, "T", T, "seed", seed)
-    layer = em.Layer(dev, shape, seed=seed)
+    layer = em.Layer(dev, shape, seed=seed, bias=bias)
     run = em.Runner(dev, shape, T, tier=em.F16)
     run.gen_inputs(seed)
     run.forward(layer, residual=False)
@@ -524,9 +546,14 @@ def _f16_case(dev, name, T, seed, sample=None):
     run.free()
     layer.free()
     h2, _ = ol.inputs(shape, seed, T)
-    toks = np.arange(T) if sample is None else np.random.default_rng(seed).choice(T, sample, replace=False)
-    hl = ol.HostLayer(shape, seed=seed, experts=[])
-    yr, idr, wtr, _ = hl.run(h2[toks], None)
+    if sample is None:
+        toks = np.arange(T)
+    else:
+        toks, big, mine = _sample_tokens(ids, T, seed, sample)
+        assert len(toks) >= sample and set(mine[:16]) <= set(toks) and set(mine[-16:]) <= set(toks)
+        _say("sampled", len(toks), "tokens; largest expert", big, "with", len(mine), "slots")
+    hl = ol.HostLayer(shape, seed=seed, experts=[], bias=bias)
+    yr, idr, wtr, _ = hl.run(h2[toks], None, nthreads=ORACLE_THREADS)
     assert np.array_equal(ids[toks], idr)  # routing is the exact tier's at every tier
     assert np.array_equal(wt[toks].view(np.uint32), wtr.view(np.uint32))
     m = ol.err_metrics(y[toks], yr)
@@ -540,31 +567,57 @@ def test_f16_tier_tolerance(dev, name, T):
     assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
 
 
-def test_f16_tier_prefill_2048_sampled(dev):
-    """config 4: 2048 tokens through the config-1 layer; 24 tokens checked against the oracle"""
-    m = _f16_case(dev, "c1", 2048, seed=0, sample=24)
+@pytest.mark.parametrize("name", ["c1", "c1k"])
+def test_f16_tier_prefill_2048_sampled(dev, name):
+    """config 4: 2048 tokens through the config-1 layer (Q8_0) and its Q4_K / Q6_K variant; 64 tokens
+    checked against the oracle, among them the first and last tiles of the most-loaded expert"""
+    m = _f16_case(dev, name, 2048, seed=0, sample=64)
     assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
 
 
 def test_f16_tier_config5_mixed(dev):
     """config 5: 512 experts top-10 with the shared expert, one decode token plus a 512-token chunk in one
-    launch, Zipf(1.1) router bias; token 0 and 15 others checked against the oracle (routing bit-exact)"""
-    shape, T, seed = em.SHAPES["c5"], 513, 5
-    bias = em.zipf_bias(shape.ne, seed)
-    _say("f16 tier c5 mixed", "T", T)
-    layer = em.Layer(dev, shape, seed=seed, bias=bias)
-    run = em.Runner(dev, shape, T, tier=em.F16)
-    run.gen_inputs(seed)
-    run.forward(layer, residual=False)
-    y, ids, wt = run.outputs()
-    run.free()
+    launch, Zipf(1.1) router bias; 64 tokens (token 0, the first and last tiles of the most-loaded expert)
+    checked against the oracle (routing bit-exact)"""
+    shape, seed = em.SHAPES["c5"], 5
+    m = _f16_case(dev, "c5", 513, seed=seed, sample=64, bias=em.zipf_bias(shape.ne, seed))
+    assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
+
+
+def test_f16_tier_down_outputs_past_f16_range(dev):
+    """the f16 tier stores each slot's down output as f16 and keeps the f32 value beside it where that
+    overflows (|v| > 65504), and the combine reads it there: with the down stack's block scales raised
+    by 2^k (the largest to 2^8), outputs pass 65504, and the f16 tier still agrees with the exact tier (f32 throughout,
+    bit-exact to the oracle elsewhere) to the tier's tolerance, with no inf"""
+    shape = em.Shape(2048, 16, 4, 256, 0, em.Q8_0, em.Q8_0, em.Q8_0)
+    T = 64
+    _say("f16 range", "T", T)
+    layer = em.Layer(dev, shape, seed=13)
+    nb = shape.stack_bytes()[2]
+    raw = dev.read(layer.D, (nb // 34, 34), np.uint8).copy()
+    h = raw[:, :2].copy().view(np.uint16)[:, 0]
+    e = (h >> 10) & 31
+    # raise every scale by 2^k, k taking the largest to 2^8: the dequantised weights (the MFMA's f16
+    # operands, |d q| <= 127 d < 2^15) stay in range while the dot products leave it
+    k = int(23 - e.max())
+    assert k >= 16 and e[(h & 0x7fff) != 0].min() > 0
+    h = np.where(h & 0x7fff, h + np.uint16(k << 10), h).astype(np.uint16)
+    raw[:, :2] = h.view(np.uint8).reshape(-1, 2)
+    dev.write(layer.D, raw)
+    out = {}
+    for tier in (em.EXACT, em.F16):
+        run = em.Runner(dev, shape, T, tier=tier)
+        run.gen_inputs(13)
+        run.forward(layer, residual=False)
+        out[tier] = run.outputs()
+        run.free()
     layer.free()
-    h2, _ = ol.inputs(shape, seed, T)
-    toks = np.concatenate([[0], np.random.default_rng(seed).choice(np.arange(1, T), 15, replace=False)])
-    yr, idr, wtr, _ = ol.HostLayer(shape, seed=seed, experts=[], bias=bias).run(h2[toks], None)
-    assert np.array_equal(ids[toks], idr)
-    assert np.array_equal(wt[toks].view(np.uint32), wtr.view(np.uint32))
-    m = ol.err_metrics(y[toks], yr)
+    (ye, ide, wte), (yf, idf, wtf) = out[em.EXACT], out[em.F16]
+    assert np.array_equal(ide, idf) and np.array_equal(wte.view(np.uint32), wtf.view(np.uint32))
+    _say("f16 range: scales x 2^", k, "max |y|", float(np.abs(ye).max()))
+    assert np.abs(ye).max() > 65504 * 2, np.abs(ye).max()
+    assert np.all(np.isfinite(yf))
+    m = ol.err_metrics(yf, ye)
     assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
 
 
