@@ -5,7 +5,7 @@ set -euo pipefail
 cd "$(dirname "$0")"
 hipcc --offload-arch=gfx950 -O3 -std=c++17 -fPIC -shared -ffp-contract=off \
   -Xclang -target-feature -Xclang -packed-fp32-ops \
-  -o libeureka_moe.so csrc/llb_moe_hip.cpp csrc/llb_moe_table.cpp csrc/llb_moe_gguf.cpp csrc/moe_exact.hip csrc/moe_decode.hip csrc/moe_q8.hip csrc/moe_synth.hip csrc/moe_gemm.hip "$@"
+  -o libeureka_moe.so csrc/llb_moe_hip.cpp csrc/llb_moe_table.cpp csrc/llb_moe_gguf.cpp csrc/moe_exact.hip csrc/moe_decode.hip csrc/moe_q8.hip csrc/moe_synth.hip csrc/moe_gemm.hip csrc/moe_noalloc.hip "$@"
 # the standalone C host for one layer (driver/moe_layer_drv.c), linked against the library in place, and
 # the code object its LLB_LAUNCH loads by name
 hipcc --offload-arch=gfx950 -O3 --genco -Xclang -target-feature -Xclang -packed-fp32-ops \

@@ -143,7 +143,8 @@ const char* llb_hip_last_error(void) { return g_err; }
 
 int llb_hip_init(int device) {
   g_err[0] = 0;
-  return hip_ok(hipSetDevice(device), "hipSetDevice");
+  const int rc = hip_ok(hipSetDevice(device), "hipSetDevice");
+  return rc ? rc : noalloc_setup(device);
 }
 int llb_hip_set_stream(void* s) {
   g_stream = (hipStream_t)s;

@@ -187,6 +187,8 @@ struct GemmArgs {
 int launch_moe_gemm(const GemmArgs& g, uint32_t fm, uint32_t mode, uint32_t grid_y, hipStream_t st);
 uint32_t gemm_bm();
 int llb_fail_msg(int code, const char* msg);  // sets llb_hip_last_error's text, returns code
+// the static scratch's device address on the current device, resolved once (moe_noalloc.hip)
+int noalloc_setup(int device);
 hipStream_t llb_cur_stream();
 // stream residency (llb_moe_gguf.cpp): stage_done waits for a token's uploads (the staging is reused)
 int stream_done();

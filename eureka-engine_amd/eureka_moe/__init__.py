@@ -73,6 +73,8 @@ _SIGS = {
     "llb_moe_hip_scratch_bytes": (C.c_size_t, [C.POINTER(MoeLayer), C.c_uint32, C.c_int]),
     "llb_moe_hip_forward": (C.c_int, [C.POINTER(MoeLayer), C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64,
                                       C.c_uint64, C.c_uint64, C.c_size_t, C.c_int]),
+    "llb_moe_hip_forward_static": (C.c_int, [C.POINTER(MoeLayer), C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64,
+                                             C.c_uint64, C.c_uint64, C.c_int]),
     "llb_moe_hip_forward_norm": (C.c_int, [C.POINTER(MoeLayer), C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64,
                                            C.c_float, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64,
                                            C.c_uint64, C.c_size_t, C.c_int]),
@@ -226,6 +228,8 @@ class Shape:
             return 0
         return self.sf * (row_bytes(self.fsg, self.dm) + row_bytes(self.fsu, self.dm)) + self.dm * row_bytes(self.fsd, self.sf)
 
+
+STATIC_SCRATCH_BYTES = 16 << 20  # LLB_MOE_STATIC_SCRATCH_BYTES (llb_moe_hip.h)
 
 SHAPES = {
     # config 1: 128 experts top-8, ef 768, Q8_0, no shared expert

@@ -130,6 +130,18 @@ int llb_moe_hip_forward_norm(const llb_moe_layer* L, uint32_t T, llb_dptr x, llb
                              llb_dptr x1, llb_dptr h2, llb_dptr y, llb_dptr ids, llb_dptr wt, llb_dptr scratch,
                              size_t scratch_bytes, int tier);
 
+/* The forward with no scratch argument and no allocation. No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The transient state lives in a device array of LLB_MOE_STATIC_SCRATCH_BYTES built into the
+ * library (one copy per device, held until the process ends; its address is resolved by llb_hip_init or
+ * by the first call on a device). Same bits as llb_moe_hip_forward. Exact and q8 tiers, resident layers
+ * (not LLB_MOE_RES_STREAM); a layer and T whose llb_moe_hip_scratch_bytes exceeds the array are refused
+ * with LLB_HIP_EINVAL. Every call on a device shares that device's array: calls that overlap on one
+ * device (several streams or host threads) race and must be serialised by the caller. */
+#define LLB_MOE_STATIC_SCRATCH_BYTES (16u << 20)
+int llb_moe_hip_forward_static(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dptr x1, llb_dptr y, llb_dptr ids,
+                               llb_dptr wt, int tier);
+
 /* The fused one-launch layer (k_fused: the four stages as work items of one persistent launch with
  * completion counters between phases) is disabled: it hung the GPU twice and the cause is not shown.
  * set_fused(0) is accepted (the three / four-launch path, the only one that runs); set_fused(on != 0)

@@ -95,3 +95,23 @@ def test_fused_path_is_refused():
     assert lib.llb_moe_hip_set_fused(1) == -1
     assert b"disabled" in lib.llb_hip_last_error() and b"hung" in lib.llb_hip_last_error()
     assert lib.llb_moe_hip_set_fused(0) == 0
+
+
+def test_forward_static_refuses_before_touching_a_device():
+    """llb_moe_hip_forward_static's argument checks (the f16 tier, a streamed layer, a scratch need past the
+    static array) answer before any device call, so they run here without a GPU"""
+    lib = C.CDLL(em.LIB_PATH)
+    f = lib.llb_moe_hip_forward_static
+    f.restype = C.c_int
+    f.argtypes = em._SIGS["llb_moe_hip_forward_static"][1]
+    lib.llb_hip_last_error.restype = C.c_char_p
+    lib.llb_moe_hip_scratch_bytes.restype = C.c_size_t
+    lib.llb_moe_hip_scratch_bytes.argtypes = [C.POINTER(em.MoeLayer), C.c_uint32, C.c_int]
+    s = em.SHAPES["c1"]
+    L = em.MoeLayer(s.dm, s.ne, s.nk, s.ef, s.sf, s.fx, s.fsg, s.fsu, s.fsd)
+    assert f(None, 1, 0, 0, 0, 0, 0, em.EXACT) == -1
+    assert f(C.byref(L), 1, 0, 0, 0, 0, 0, em.F16) == -1 and b"f16" in lib.llb_hip_last_error()
+    assert lib.llb_moe_hip_scratch_bytes(C.byref(L), 4096, em.EXACT) > em.STATIC_SCRATCH_BYTES
+    assert f(C.byref(L), 4096, 0, 0, 0, 0, 0, em.EXACT) == -1 and b"static array" in lib.llb_hip_last_error()
+    L.res = 2  # LLB_MOE_RES_STREAM
+    assert f(C.byref(L), 1, 0, 0, 0, 0, 0, em.EXACT) == -1 and b"streamed" in lib.llb_hip_last_error()
