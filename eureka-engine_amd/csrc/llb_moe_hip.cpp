@@ -649,8 +649,15 @@ static bool dec_ok(const llb_moe_layer* L) {
     return false;
   return true;
 }
+// the q8 tier's decode layer on the same kernels needs its down launch to take the layer (it has no
+// general fallback of the same numerics)
+static bool dec_q8_ok(const llb_moe_layer* L) {
+  const uint32_t fd = L->fx >> 8 & 15;
+  return dec_ok(L) && dn_dec_lds(L->nk, L->ef, L->sf, row_bytes(fd, L->ef), L->sf ? row_bytes(L->fsd, L->sf) : 0,
+                                 L->dm, L->sf != 0, true, nullptr, nullptr) != 0;
+}
 static int decode_forward(const llb_moe_layer* L, const float* h2, const float* x1, float* y, uint32_t* ids,
-                          float* wt, uint8_t* sc, const ExactScratch& s, const NormIn* nin) {
+                          float* wt, uint8_t* sc, const ExactScratch& s, const NormIn* nin, bool q8) {
   const uint32_t fg = L->fx & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
   TopkArgs tk{};
   int rc = route(L, 1, h2, ids, wt, sc, s, false, &tk, nin, true);
@@ -680,7 +687,8 @@ static int decode_forward(const llb_moe_layer* L, const float* h2, const float* 
   g.stamps = g_dec_stamps;
 #endif
   stage_begin(ST_GU);
-  if ((rc = launched(launch_gu_dec(g, fg, L->sf ? L->fsg : 0, g_stream), "top-k + expert gate/up (decode)"))) return rc;
+  if ((rc = launched(launch_gu_dec(g, fg, L->sf ? L->fsg : 0, q8, g_stream), "top-k + expert gate/up (decode)")))
+    return rc;
   stage_end(ST_GU);
   DecDnArgs d{};
   d.D = dp<uint8_t>(L->D);
@@ -702,8 +710,8 @@ static int decode_forward(const llb_moe_layer* L, const float* h2, const float* 
   d.stamps = g_dec_stamps;
 #endif
   stage_begin(ST_DN);
-  int lr = launch_dn_dec(d, fd, L->sf ? L->fsd : 0, g_stream);
-  if (lr) {  // more down tasks or wider rows than its LDS holds: the general down kernel, same inputs
+  int lr = launch_dn_dec(d, fd, L->sf ? L->fsd : 0, q8, g_stream);
+  if (lr && !q8) {  // more down tasks or wider rows than its LDS holds: the general down kernel, same inputs
     DnArgs o{};
     o.D = d.D;
     o.rbd = d.rbd;
@@ -751,8 +759,11 @@ static int forward_impl(const llb_moe_layer* L, uint32_t T, llb_dptr h2, llb_dpt
   const bool streamed = L->res == LLB_MOE_RES_STREAM;
   if (streamed && (tier != LLB_MOE_EXACT || T != 1 || g_capturing))
     return fail(LLB_HIP_EINVAL, "stream residency: the exact tier, one token, outside graph capture");
-  if (tier == LLB_MOE_EXACT && T == 1 && !streamed && dec_ok(L))
-    return decode_forward(L, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt), sc, s, nin);
+  // one token on the decode kernels: the exact tier, and the q8 tier (the same launches with q8_1
+  // activations and integer dots)
+  if (T == 1 && !streamed && ((tier == LLB_MOE_EXACT && dec_ok(L)) || (tier == LLB_MOE_Q8 && dec_q8_ok(L))))
+    return decode_forward(L, dp<float>(h2), dp<float>(x1), dp<float>(y), dp<uint32_t>(ids), dp<float>(wt), sc, s, nin,
+                          tier == LLB_MOE_Q8);
   TopkArgs tk{};
   const bool fuse_topk = (tier == LLB_MOE_Q8 || fg == fu) && T == 1 && !streamed;
   // the q8 tier computes the shared gate / up rows in its own gate / up launch (int8 dots)

@@ -25,6 +25,7 @@
 // The activations a lane multiplies (its group's 64 columns) stay in registers for all its rows.
 #include "moe_dev.h"
 #include "moe_kernels.h"
+#include "moe_q8dot.h"
 
 // per-block wall-clock stamps for latency studies (100 MHz): a build that defines MOE_PHASE_T records
 // stamp i of block b of thread 0 (and of thread 64, stamps >= 8 of k_gu_dec) in dec_stamp[i][b]; the
@@ -560,6 +561,42 @@ int launch_router(const TreeArgs& a, u32 nq, hipStream_t st) {
   return -1;
 }
 
+// ---------------------------------------------------------------- the q8 tier's activations and dots
+
+// q8_1 (pf_q8x's quantizer) of 4 consecutive values a lane, eight lanes a 32-block (lanes 8 m .. 8 m + 7
+// hold block m's float4s in column order): d = amax / 127, q = roundf(x / d) in [-127, 127], s = the
+// block's sum (in lane-group order: the q8 tier's sums are checked to a tolerance, not to an order).
+// Returns the four codes packed; d and s come back on every lane of the group.
+DEV u32 q8_quad(float4 x, float& d_out, float& s_out) {
+  float a = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+  float s = (x.x + x.y) + (x.z + x.w);
+#pragma unroll
+  for (u32 m = 1; m < 8; m <<= 1) {
+    a = fmaxf(a, __shfl_xor(a, m, 64));
+    s = s + __shfl_xor(s, m, 64);
+  }
+  const float d = a / 127.0f;
+  auto code = [&](float v) -> u32 {
+    return a == 0.0f ? 0u : (u32)(u8)(signed char)max(-127, min(127, (int)roundf(v / d)));
+  };
+  d_out = d;
+  s_out = s;
+  return code(x.x) | code(x.y) << 8 | code(x.z) << 16 | code(x.w) << 24;
+}
+
+// blocks 2 q and 2 q + 1 of a row (its bytes at rp, in LDS) against the q8_1 activations xq / xd (LDS)
+template <u32 F> DEV float pair_blocks_q8(const u8* rp, u32 q, const u32* xq, const float2* xd) {
+  float v = 0.0f;
+#pragma unroll
+  for (u32 bb = 0; bb < 2; bb++) {
+    const u32 b = 2 * q + bb;
+    const uint4 x0 = lds16((const u8*)(xq + 8 * b)), x1 = lds16((const u8*)(xq + 8 * b + 4));
+    const u32 x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    v += blk_q8<F>(rp, b, x, xd[b]);
+  }
+  return v;
+}
+
 // ---------------------------------------------------------------- gate / up (+ SwiGLU), one token
 
 // LDS of k_gu_dec (bytes): x (dm = 2048, padded) | routing: ids [64], candidates [64] u64 | the pairs'
@@ -619,13 +656,22 @@ DEV float pair_dots(const PairChunks<RB>& pc, u8* stage, float* lv, const float*
   WAVE_FENCE();
   return pair_compute<F, RB, TREE>(stage, lv, xs, L);
 }
+// the q8 tier's pair: lane q of each half takes blocks 2 q, 2 q + 1 of its row; the 32 partial sums meet
+// in an xor tree (lane 0: the gate dot, lane 32: the up dot)
+template <u32 F, u32 RB>
+DEV float pair_compute_q8(const u8* stage, const u32* xq, const float2* xd, u32 L) {
+  float v = pair_blocks_q8<F>(stage + (L >> 5) * RB, L & 31, xq, xd);
+#pragma unroll
+  for (u32 m = 16; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
 
 // A block of 16 waves takes 16 consecutive features of one slot, one a wave: the feature's gate row on
 // lanes 0..31 and its up row on lanes 32..63, each lane one 64-column group. Wave 0 routes the token
 // first (every block recomputes it; block 0 writes ids / wt / sgo). The shared expert's gate / up rows
 // (tree order) are spread over the blocks, waves 1, 2, ... taking shared feature b, b + nblocks, ...
 // (their loads go out before the routing is known). SwiGLU is applied once a block, a lane a feature.
-template <u32 F, u32 FS, u32 NI>
+template <u32 F, u32 FS, u32 NI, bool Q8>
 __global__ void __launch_bounds__(1024) k_gu_dec(DecGuArgs a) {
   extern __shared__ uint4 dsm[];
   DSTAMP(0);
@@ -672,6 +718,18 @@ __global__ void __launch_bounds__(1024) k_gu_dec(DecGuArgs a) {
     __syncthreads();
     ids_s = tk_id;
   }
+  // the q8 tier: x as q8_1 over the x copy (whose float values this tier does not read): codes [2048],
+  // then {d, s} [64]; waves 0 .. 7 hold x in xv
+  u32* xq = (u32*)xs;
+  float2* xd = (float2*)(sm + DEC_DM);
+  if constexpr (Q8) {
+    if (tid < 512) {
+      float d, sum;
+      xq[tid] = q8_quad(xv, d, sum);
+      if ((tid & 7u) == 0) xd[tid >> 3] = make_float2(d, sum);
+    }
+    __syncthreads();
+  }
   DSTAMP(1);
   DSTAMP(2);
   DSTAMP(8);
@@ -682,7 +740,14 @@ __global__ void __launch_bounds__(1024) k_gu_dec(DecGuArgs a) {
   const u32 q = L & 31;
   if constexpr (FS != 0) {
     if (has_s) {
-      const float sv = pair_dots<FS, RBS, true>(sc, stage, lv, xs, L);
+      float sv;
+      if constexpr (Q8) {
+        sc.store(stage, L);
+        WAVE_FENCE();
+        sv = pair_compute_q8<FS, RBS>(stage, xq, xd, L);
+      } else {
+        sv = pair_dots<FS, RBS, true>(sc, stage, lv, xs, L);
+      }
       if (L == 0) gus[2 * (16 + w - 1)] = sv;
       if (L == 32) gus[2 * (16 + w - 1) + 1] = sv;
       WAVE_FENCE();
@@ -711,7 +776,9 @@ __global__ void __launch_bounds__(1024) k_gu_dec(DecGuArgs a) {
     touch = *(const u32*)(live ? lo + 128 * L : a.D);
     __builtin_amdgcn_sched_barrier(0);
   }
-  const float sv = pair_compute<F, RB, false>(stage, lv, xs, L);
+  float sv;
+  if constexpr (Q8) sv = pair_compute_q8<F, RB>(stage, xq, xd, L);
+  else sv = pair_compute<F, RB, false>(stage, lv, xs, L);
   if (L == 0) gus[2 * w] = sv;
   if (L == 32) gus[2 * w + 1] = sv;
   DSTAMP(4);
@@ -784,7 +851,27 @@ DEV void dn_rows(const u8* rows, u64 rb, u32 cols, u32 nrow, const float* xw, fl
   }
 }
 
-template <u32 FD, u32 FS>
+// the q8 tier's rows: lane (rho, q) takes blocks 2 q, 2 q + 1 of row rho of the pass; the row's lpr
+// partial sums go through LDS (lpr need not be a power of two) and its first lane adds them in order
+template <u32 F>
+DEV void dn_rows_q8(const u8* rows, u64 rb, u32 cols, u32 nrow, const u32* xq, const float2* xd, float* lv,
+                    float* part, u32 w, u32 L) {
+  const u32 lpr = cols / 64, rpp = 64 / lpr, rho = L / lpr, q = L % lpr;
+  for (u32 p0 = 0; p0 < nrow; p0 += rpp) {
+    const u32 rr = p0 + rho;
+    const bool live = rho < rpp && rr < nrow;
+    lv[L] = live ? pair_blocks_q8<F>(rows + rr * rb, q, xq, xd) : 0.0f;
+    WAVE_FENCE();
+    if (live && q == 0) {
+      float v = lv[L];
+      for (u32 i = 1; i < lpr; i++) v += lv[L + i];
+      part[rr * 16 + w] = v;
+    }
+    WAVE_FENCE();
+  }
+}
+
+template <u32 FD, u32 FS, bool Q8>
 __global__ void __launch_bounds__(1024) k_dn_dec(DecDnArgs a) {
   extern __shared__ uint4 dsm[];
   u8* sm = (u8*)dsm;
@@ -814,7 +901,17 @@ __global__ void __launch_bounds__(1024) k_dn_dec(DecDnArgs a) {
   DSTAMP(17);
   // the wave's activations: act_j or sa, coalesced, to its padded LDS copy
   const float4* xsrc = (const float4*)(shared ? a.sa : a.act + (u64)w * a.ef);
-  for (u32 i = L; i < cols / 4; i += 64) *(float4*)(xw + xpad(4 * i)) = xsrc[i];
+  u32* xq = (u32*)xw;  // the q8 tier: codes [cols], then {d, s} [cols / 32]
+  float2* xd = (float2*)(xq + cols / 4);
+  if constexpr (Q8) {
+    for (u32 i = L; i < cols / 4; i += 64) {  // cols % 256 == 0: every lane takes part in each round
+      float d, sum;
+      xq[i] = q8_quad(xsrc[i], d, sum);
+      if ((i & 7u) == 0) xd[i >> 3] = make_float2(d, sum);
+    }
+  } else {
+    for (u32 i = L; i < cols / 4; i += 64) *(float4*)(xw + xpad(4 * i)) = xsrc[i];
+  }
   // the combine's inputs
   const float wtv = tid < nk ? a.wt[tid] : 0.0f;
   const float sgv = FS ? a.sgo[0] : 0.0f;
@@ -823,7 +920,13 @@ __global__ void __launch_bounds__(1024) k_dn_dec(DecDnArgs a) {
   wait_vm0();  // the rows are in LDS
   DSTAMP(19);
   const u8* rows = stage + (a0 - a16);
-  if (shared) {
+  if constexpr (Q8) {
+    if (shared) {
+      if constexpr (FS != 0) dn_rows_q8<FS>(rows, rb, cols, nrow, xq, xd, lv, part, w, L);
+    } else {
+      dn_rows_q8<FD>(rows, rb, cols, nrow, xq, xd, lv, part, w, L);
+    }
+  } else if (shared) {
     if constexpr (FS != 0) dn_rows<FS>(rows, rb, cols, nrow, xw, lv, part, w, L);
   } else {
     dn_rows<FD>(rows, rb, cols, nrow, xw, lv, part, w, L);
@@ -843,18 +946,18 @@ __global__ void __launch_bounds__(1024) k_dn_dec(DecDnArgs a) {
 
 // ---------------------------------------------------------------- launchers
 
-template <u32 F, u32 FS>
+template <u32 F, u32 FS, bool Q8>
 static int gu_dec_one(const DecGuArgs& a, hipStream_t st) {
   constexpr u32 RB = rb2048(F), RBS = rb2048(FS);
   constexpr size_t lds = gu_lds(RB > RBS ? RB : RBS);
   static_assert(lds <= 160 * 1024, "LDS of the gate / up block");
   static bool set = false;
   if (!set) {
-    if (hipFuncSetAttribute((const void*)k_gu_dec<F, FS, 4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+    if (hipFuncSetAttribute((const void*)k_gu_dec<F, FS, 4, Q8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
             hipSuccess ||
-        hipFuncSetAttribute((const void*)k_gu_dec<F, FS, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+        hipFuncSetAttribute((const void*)k_gu_dec<F, FS, 8, Q8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
             hipSuccess ||
-        hipFuncSetAttribute((const void*)k_gu_dec<F, FS, 16>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+        hipFuncSetAttribute((const void*)k_gu_dec<F, FS, 16, Q8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
             hipSuccess) {
       (void)hipGetLastError();
       return -1;
@@ -862,18 +965,19 @@ static int gu_dec_one(const DecGuArgs& a, hipStream_t st) {
     set = true;
   }
   // experts a lane holds in top-k (ne / 64, rounded up to 4, 8 or 16)
-  if (a.tk.ne <= 256) LAUNCH_K((k_gu_dec<F, FS, 4>), dim3(a.nrb), dim3(64 * GU_WAVES), lds, st, a);
-  else if (a.tk.ne <= 512) LAUNCH_K((k_gu_dec<F, FS, 8>), dim3(a.nrb), dim3(64 * GU_WAVES), lds, st, a);
-  else LAUNCH_K((k_gu_dec<F, FS, 16>), dim3(a.nrb), dim3(64 * GU_WAVES), lds, st, a);
+  if (a.tk.ne <= 256) LAUNCH_K((k_gu_dec<F, FS, 4, Q8>), dim3(a.nrb), dim3(64 * GU_WAVES), lds, st, a);
+  else if (a.tk.ne <= 512) LAUNCH_K((k_gu_dec<F, FS, 8, Q8>), dim3(a.nrb), dim3(64 * GU_WAVES), lds, st, a);
+  else LAUNCH_K((k_gu_dec<F, FS, 16, Q8>), dim3(a.nrb), dim3(64 * GU_WAVES), lds, st, a);
   return 0;
 }
 
-int launch_gu_dec(DecGuArgs a, u32 f, u32 fs, hipStream_t st) {
+int launch_gu_dec(DecGuArgs a, u32 f, u32 fs, bool q8, hipStream_t st) {
   if (a.dm != DEC_DM || a.ef % GU_WAVES || a.tk.ne > 1024 || a.tk.nk > 64) return -1;
   a.nrb = a.nk * a.ef / GU_WAVES;
   // the shared features: at most 15 a block (waves 1 .. 15)
   if (fs && a.sf > 15 * a.nrb) return -1;
-#define GU_FS(F, FS) if (f == F && fs == FS) return gu_dec_one<F, FS>(a, st);
+#define GU_FS(F, FS) \
+  if (f == F && fs == FS) return q8 ? gu_dec_one<F, FS, true>(a, st) : gu_dec_one<F, FS, false>(a, st);
 #define GU_F(F) GU_FS(F, 0u) GU_FS(F, FM_Q4_K) GU_FS(F, FM_Q5_K) GU_FS(F, FM_Q6_K)
   GU_F(FM_Q8_0) GU_F(FM_Q4_K) GU_F(FM_Q5_K) GU_F(FM_Q6_K)
 #undef GU_F
@@ -881,31 +985,45 @@ int launch_gu_dec(DecGuArgs a, u32 f, u32 fs, hipStream_t st) {
   return -1;
 }
 
-template <u32 FD, u32 FS>
+template <u32 FD, u32 FS, bool Q8>
 static int dn_dec_one(const DecDnArgs& a, u32 nt, size_t lds, hipStream_t st) {
   static size_t set = 0;  // the dynamic LDS the kernel is allowed so far
   if (lds > set) {
-    if (hipFuncSetAttribute((const void*)k_dn_dec<FD, FS>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+    if (hipFuncSetAttribute((const void*)k_dn_dec<FD, FS, Q8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
         hipSuccess) {
       (void)hipGetLastError();
       return -1;
     }
     set = lds;
   }
-  LAUNCH_K((k_dn_dec<FD, FS>), dim3((a.dm + DN_RB - 1) / DN_RB), dim3(64 * nt), lds, st, a);
+  LAUNCH_K((k_dn_dec<FD, FS, Q8>), dim3((a.dm + DN_RB - 1) / DN_RB), dim3(64 * nt), lds, st, a);
   return 0;
 }
 
-int launch_dn_dec(DecDnArgs a, u32 fd, u32 fs, hipStream_t st) {
+// the down launch's LDS for these shapes, or 0 when it cannot take them
+size_t dn_dec_lds(u32 nk, u32 ef, u32 sf, u64 rbd, u64 rbs, u32 dm, bool shared, bool q8, u32* stage_bytes,
+                  u32* xw_bytes) {
+  const u32 nt = nk + (shared ? 1u : 0u);
+  const u32 cm = q8 ? 256u : 128u;  // (the q8 tier quantizes a wave's activations 256 at a time)
+  if (nt > 16 || ef % cm || ef > 4096 || (shared && (sf % cm || sf > 4096)) || dm % DN_RB) return 0;
+  const u64 rbmax = rbd > rbs ? rbd : rbs;
+  const u32 sb = (u32)((DN_RB * rbmax + 32 + 15) & ~(u64)15);
+  const u32 cmax = ef > sf ? ef : sf;
+  // float activations, padded (exact), or q8_1 codes and {d, s} (q8)
+  const u32 xb = q8 ? (cmax + cmax / 32 * 8 + 15) & ~15u : (cmax + cmax / 16) * 4;
+  const size_t lds = DN_PART + (size_t)nt * (sb + xb + 4096);
+  if (lds > 160 * 1024 - 256) return 0;  // (and 64 bytes of static LDS)
+  if (stage_bytes) *stage_bytes = sb;
+  if (xw_bytes) *xw_bytes = xb;
+  return lds;
+}
+
+int launch_dn_dec(DecDnArgs a, u32 fd, u32 fs, bool q8, hipStream_t st) {
   const u32 nt = a.nk + (fs ? 1u : 0u);
-  if (nt > 16 || a.ef % 128 || a.ef > 4096 || (fs && (a.sf % 128 || a.sf > 4096)) || a.dm % DN_RB) return -1;
-  const u64 rbmax = a.rbd > a.rbs ? a.rbd : a.rbs;
-  a.stage_bytes = (u32)((DN_RB * rbmax + 32 + 15) & ~(u64)15);
-  const u32 cmax = a.ef > a.sf ? a.ef : a.sf;
-  a.xw_bytes = (cmax + cmax / 16) * 4;
-  const size_t lds = DN_PART + (size_t)nt * (a.stage_bytes + a.xw_bytes + 4096);
-  if (lds > 160 * 1024 - 256) return -1;  // (and 64 bytes of static LDS)
-#define DN_FS(FD, FS) if (fd == FD && fs == FS) return dn_dec_one<FD, FS>(a, nt, lds, st);
+  const size_t lds = dn_dec_lds(a.nk, a.ef, a.sf, a.rbd, a.rbs, a.dm, fs != 0, q8, &a.stage_bytes, &a.xw_bytes);
+  if (!lds) return -1;
+#define DN_FS(FD, FS) \
+  if (fd == FD && fs == FS) return q8 ? dn_dec_one<FD, FS, true>(a, nt, lds, st) : dn_dec_one<FD, FS, false>(a, nt, lds, st);
 #define DN_F(FD) DN_FS(FD, 0u) DN_FS(FD, FM_Q4_K) DN_FS(FD, FM_Q5_K) DN_FS(FD, FM_Q6_K)
   DN_F(FM_Q8_0) DN_F(FM_Q4_K) DN_F(FM_Q5_K) DN_F(FM_Q6_K)
 #undef DN_F

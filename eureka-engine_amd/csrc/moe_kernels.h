@@ -120,8 +120,11 @@ struct DecDnArgs {
 extern unsigned long long* g_dec_stamps;
 #endif
 int launch_router(const TreeArgs& a, uint32_t nq, hipStream_t st);
-int launch_gu_dec(DecGuArgs a, uint32_t f, uint32_t fs, hipStream_t st);
-int launch_dn_dec(DecDnArgs a, uint32_t fd, uint32_t fs, hipStream_t st);
+// q8: the q8 tier's dots (q8_1 activations, v_dot4) in place of the exact tier's f32 orders
+int launch_gu_dec(DecGuArgs a, uint32_t f, uint32_t fs, bool q8, hipStream_t st);
+int launch_dn_dec(DecDnArgs a, uint32_t fd, uint32_t fs, bool q8, hipStream_t st);
+size_t dn_dec_lds(uint32_t nk, uint32_t ef, uint32_t sf, uint64_t rbd, uint64_t rbs, uint32_t dm, bool shared, bool q8,
+                  uint32_t* stage_bytes, uint32_t* xw_bytes);
 
 struct FusedArgs {
   TreeArgs tr;

@@ -358,9 +358,9 @@ def test_q8_tier_tolerance(dev, name, T):
 
 
 def test_q8_tier_same_bits_every_path(dev):
-    """the q8 tier's three launch shapes give the same bits token for token: one token (top-k inside the
-    gate / up launch, activations quantized in LDS), eight tokens (quantized in LDS), nine tokens (the
-    q8_1 launches)"""
+    """the q8 tier's batched launch shapes give the same bits token for token: eight tokens (activations
+    quantized in LDS) and nine tokens (the q8_1 launches); one token runs on the decode kernels, whose
+    sums go in another order: the same routing bits and outputs within the tier's tolerance"""
     shape = em.SHAPES["c2"]
     layer = em.Layer(dev, shape, seed=4)
     ys = {}
@@ -372,9 +372,34 @@ def test_q8_tier_same_bits_every_path(dev):
         ys[T] = run.outputs()
         run.free()
     layer.free()
-    for a, b, n in ((1, 9, 1), (8, 9, 8)):
-        for u, v in zip(ys[a], ys[b]):
-            assert np.array_equal(np.asarray(u[:n]).view(np.uint32), np.asarray(v[:n]).view(np.uint32)), (a, b)
+    for u, v in zip(ys[8], ys[9]):
+        assert np.array_equal(np.asarray(u[:8]).view(np.uint32), np.asarray(v[:8]).view(np.uint32))
+    (y1, i1, w1), (y9, i9, w9) = ys[1], ys[9]
+    assert np.array_equal(i1[:1], i9[:1]) and np.array_equal(w1[:1].view(np.uint32), w9[:1].view(np.uint32))
+    m = ol.err_metrics(y1[:1], y9[:1])
+    assert m["max_rel"] < 1e-3 and m["cos"] >= 0.99999, m
+
+
+@pytest.mark.parametrize("si", range(len(DECODE_SMALL)))
+def test_q8_decode_small_against_oracle(dev, si):
+    """the q8 tier's one-token layer (the decode kernels with q8_1 activations and v_dot4) against the
+    oracle's q8 mode, every routed and shared format the decode kernels take"""
+    shape = DECODE_SMALL[si]
+    _say("q8 decode", si, "T 1")
+    layer = em.Layer(dev, shape, seed=400 + si)
+    run = em.Runner(dev, shape, 1, tier=em.Q8)
+    run.gen_inputs(400 + si)
+    run.forward(layer)
+    y, ids, wt = run.outputs()
+    run.free()
+    layer.free()
+    h2, x1 = ol.inputs(shape, 400 + si, 1)
+    hl = ol.HostLayer(shape, seed=400 + si, experts=[])
+    yq, idq, wtq, _ = hl.run(h2, x1, tier="q8")
+    assert np.array_equal(ids, idq) and np.array_equal(wt.view(np.uint32), wtq.view(np.uint32))
+    m = ol.err_metrics(y, yq)
+    _say("q8 decode vs oracle q8", m)
+    assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
 
 
 @pytest.mark.parametrize("name,T,tier", [("c2", 1, em.EXACT), ("c2", 1, em.Q8), ("c2", 40, em.F16), ("c5", 33, em.F16)])
