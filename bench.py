@@ -130,14 +130,20 @@ def stage_bytes(shape, T=1, shared_in_gu=True):
 MFMA_F16_PEAK_TFS = 2500.0
 
 
-def prefill(dev, shape, T, layers, steps, warmup, name=""):
+MFMA_I8_PEAK_TOPS = 5000.0
+
+
+def prefill(dev, shape, T, layers, steps, warmup, name="", tier=None):
     """T-token chunks through `layers` resident layers on the f16 MFMA tier (stacks packed once,
-    outside the timer): tokens/s, and the gate/up GEMM's MFMA rate (algorithmic flops 2 T nk dm ef x 2
-    per launch over its HIP-event time)."""
+    outside the timer) or the q8 tier: tokens/s, and the gate/up kernel's rate (algorithmic flops
+    2 T nk dm ef x 2 per launch over its HIP-event time) against the f16 MFMA peak (f16 tier) or the
+    int8 MFMA peak (q8 tier, whose products run on v_dot4 rather than the matrix cores)."""
+    tier = em.F16 if tier is None else tier
     Ls = [em.Layer(dev, shape, seed=1, layer=100 + i) for i in range(layers)]
-    for L in Ls:
-        L.pack()
-    run = em.Runner(dev, shape, T, tier=em.F16)
+    if tier == em.F16:
+        for L in Ls:
+            L.pack()
+    run = em.Runner(dev, shape, T, tier=tier)
     run.gen_inputs(1)
     dev.sync()
     for _ in range(warmup):
@@ -164,12 +170,14 @@ def prefill(dev, shape, T, layers, steps, warmup, name=""):
     for L in Ls:
         L.free()
     us_layer = wall / (steps * layers) * 1e6
+    peak = MFMA_F16_PEAK_TFS if tier == em.F16 else MFMA_I8_PEAK_TOPS
+    kern = "gate_up GEMM (f16 MFMA)" if tier == em.F16 else "gate_up (int8 v_dot4 on q8_1 activations)"
     return {"tokens_per_s": round(T / (us_layer * 1e-6), 1), "us_per_layer_chunk": round(us_layer, 2), "T": T,
             "layers": layers, "stages_us": {k: round(v[0], 2) for k, v in st.items()},
-            "roofline": {"bound": "mfma", "kernel": "gate_up GEMM (f16 MFMA)", "achieved": round(ach, 1),
-                         "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFS, 4),
-                         "traffic": measured_traffic(f"{name}_prefill_{T}", "gate_up"), "kernel_us": round(gu_us, 2),
-                         "weight_gbs": round(wbytes / (gu_us * 1e-6) / 1e9, 1)}}
+            "roofline": {"bound": "mfma", "kernel": kern, "achieved": round(ach, 1),
+                         "peak": peak, "unit": "TFLOP/s" if tier == em.F16 else "TOP/s", "frac": round(ach / peak, 4),
+                         "traffic": measured_traffic(f"{name}_prefill_{T}", "gate_up", tier == em.F16),
+                         "kernel_us": round(gu_us, 2), "weight_gbs": round(wbytes / (gu_us * 1e-6) / 1e9, 1)}}
 
 
 def batched(dev, shape, T, layers, steps, warmup, tier):
@@ -377,10 +385,11 @@ def main():
     ap.add_argument("--prefill-T", type=int, default=2048)
     ap.add_argument("--no-c5", dest="c5", action="store_false",
                     help="skip the config-5 leg (48 resident 512-expert layers, 1 + 512 tokens a launch)")
-    ap.add_argument("--legs", default="q8,step,batched,prefill,prefill_k,c5,rmsnorm,residency,copy",
+    ap.add_argument("--legs", default="q8,step,batched,prefill,prefill_k,prefill_q8,c5,rmsnorm,residency,copy",
                     help="legs after the decode line: q8 (the int8 tier's decode), step (the decode step with the "
                          "input step, two calls or one), batched (config 3), prefill (c1), "
-                         "prefill_k (c1k), c5, rmsnorm, residency (GGUF stacks in each residency mode), copy "
+                         "prefill_k (c1k), prefill_q8 (c1 on the q8 tier), c5, rmsnorm, residency (GGUF stacks in each "
+                         "residency mode), copy "
                          "(achievable HBM bandwidth)")
     ap.add_argument("--traffic-from", metavar="DIR",
                     help="only write profiles/traffic.json from the PMC csv directories under DIR and exit")
@@ -396,7 +405,7 @@ def main():
         return
     legs = set(args.legs.split(",")) if args.legs else set()
     if not args.prefill:
-        legs -= {"batched", "prefill", "prefill_k"}
+        legs -= {"batched", "prefill", "prefill_k", "prefill_q8"}
     if not args.c5:
         legs.discard("c5")
     if args.copy_calib:
@@ -574,6 +583,12 @@ def main():
         pshape = em.SHAPES[args.prefill_config]
         out["prefill"] = prefill(dev, pshape, args.prefill_T, 4, max(2, args.steps // 4), 1, args.prefill_config)
         out["prefill"]["config"] = f"{args.prefill_config} layer, {args.prefill_T}-token chunk, f16 MFMA tier, packed stacks"
+    if "prefill_q8" in legs:
+        # the q8 tier (the reference's LLB_PREFILL=fast numerics: q8_1 activations, integer block dots)
+        out["prefill_q8"] = prefill(dev, em.SHAPES[args.prefill_config], args.prefill_T, 2, max(2, args.steps // 8), 1,
+                                    args.prefill_config, tier=em.Q8)
+        out["prefill_q8"]["config"] = (f"{args.prefill_config} layer, {args.prefill_T}-token chunk, q8 tier "
+                                       f"(q8_1 activations, v_dot4 block dots), GGUF stacks")
     if "prefill_k" in legs:
         # the same layer shape with Q4_K gate / up and Q6_K down weight tiles
         out["prefill_k_quants"] = prefill(dev, em.SHAPES["c1k"], args.prefill_T, 4, max(2, args.steps // 4), 1, "c1k")

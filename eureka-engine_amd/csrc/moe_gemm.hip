@@ -461,7 +461,8 @@ __global__ void __launch_bounds__(256, g3_blocks(F, MODE, PKD)) k_moe_gemm3(Gemm
 
 // y[t][r] = (sum_j, rank order, wt[t][j] out[inv[t nk + j]][r]) + sgo[t] shd[t][r] + x1[t][r]; the slots'
 // down outputs in f16 (half the bytes of the largest intermediate), their weighted sum in f32
-__global__ void __launch_bounds__(256) k_combine(const _Float16* __restrict__ out, const float* __restrict__ spill,
+template <typename OT>
+__global__ void __launch_bounds__(256) k_combine(const OT* __restrict__ out, const float* __restrict__ spill,
                                                  const u32* __restrict__ inv,
                                                  const float* __restrict__ wt, u32 nk, const float* __restrict__ shd,
                                                  const float* __restrict__ sgo, const float* __restrict__ x1,
@@ -485,12 +486,16 @@ __global__ void __launch_bounds__(256) k_combine(const _Float16* __restrict__ ou
       if (j0 + j < nk) {
         typedef _Float16 h4 __attribute__((ext_vector_type(4)));
         const u64 so = (u64)srow[j0 + j] * dm + r;
-        const h4 hv = *(const h4*)(out + so);
-        v[j] = make_float4((float)hv[0], (float)hv[1], (float)hv[2], (float)hv[3]);
-        if (__builtin_isinf(v[j].x)) v[j].x = spill[so];
-        if (__builtin_isinf(v[j].y)) v[j].y = spill[so + 1];
-        if (__builtin_isinf(v[j].z)) v[j].z = spill[so + 2];
-        if (__builtin_isinf(v[j].w)) v[j].w = spill[so + 3];
+        if constexpr (sizeof(OT) == 4) {
+          v[j] = *(const float4*)(out + so);
+        } else {
+          const h4 hv = *(const h4*)(out + so);
+          v[j] = make_float4((float)hv[0], (float)hv[1], (float)hv[2], (float)hv[3]);
+          if (__builtin_isinf(v[j].x)) v[j].x = spill[so];
+          if (__builtin_isinf(v[j].y)) v[j].y = spill[so + 1];
+          if (__builtin_isinf(v[j].z)) v[j].z = spill[so + 2];
+          if (__builtin_isinf(v[j].w)) v[j].w = spill[so + 3];
+        }
       }
 #pragma unroll
     for (u32 j = 0; j < 8; j++) {
@@ -514,6 +519,260 @@ __global__ void __launch_bounds__(256) k_combine(const _Float16* __restrict__ ou
     yv = make_float4(mo.x + res.x, mo.y + res.y, mo.z + res.z, mo.w + res.w);
   }
   *(float4*)(y + o) = yv;
+}
+
+// ---------------------------------------------------------------- the q8 tier's grouped GEMM (int8 MFMA)
+//
+// The q8 tier for many tokens (the reference's LLB_PREFILL=fast numerics, host/llb_pf.cuh:447-620): the
+// slots grouped by expert as for the f16 tier, the activations as q8_1 (codes, {d, s} a 32-column block),
+// the weights' codes straight from the GGUF blocks. A 32-column block's integer dot I (codes x codes) is
+// one v_mfma_i32_32x32x32_i8 per 32 x 32 tile, exact; the block's value d_w d_x I - m_w s (mx_blk,
+// host/llb_pf.cuh:468-515) goes into an f32 accumulator in the epilogue of every block. Q6_K's two
+// 16-column scales take two v_mfma_i32_32x32x16_i8 a block. Tile and block order as k_moe_gemm3: 64 slots
+// (one or two live 32-row fragments) x 256 weight rows (mode 0: 128 gate + 128 up features, SwiGLU in the
+// epilogue), four waves, wave w the weight rows of features 32 w .. (mode 0) or rows 64 w .. (mode 1).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+// a lane's codes of block b of a weight row (GGUF bytes at row): columns 16 h .. 16 h + 15 as 16 signed
+// bytes, and the block's scale dw and min mw (the block's value is dw d_x I - mw s)
+template <u32 F> DEV void i8_codes(const u8* row, u32 b, u32 h, i32x4& c, float& dw, float& mw);
+// Q8_0: the 16 code bytes [p, p + 16) exactly (a block is 34 bytes, so p is 2- or 4-aligned): four
+// dwords, or a u16, three dwords and a u16. No byte past them is read: past the last block of the last
+// row lies the end of the stack.
+template <> DEV void i8_codes<FM_Q8_0>(const u8* row, u32 b, u32 h, i32x4& c, float& dw, float& mw) {
+  const u8* B = row + 34u * b;
+  const u8* p = B + 2 + 16 * h;
+  if (((uintptr_t)p & 2u) == 0) {
+    const u32* a = (const u32*)p;
+#pragma unroll
+    for (int k = 0; k < 4; k++) c[k] = (int)a[k];
+  } else {
+    const u32* m = (const u32*)(p + 2);
+    const u32 lo = ld_u16(p), m0 = m[0], m1 = m[1], m2 = m[2], hi = ld_u16(p + 14);
+    c[0] = (int)(lo | m0 << 16);
+    c[1] = (int)(m0 >> 16 | m1 << 16);
+    c[2] = (int)(m1 >> 16 | m2 << 16);
+    c[3] = (int)(m2 >> 16 | hi << 16);
+  }
+  dw = f16v(ld_u16(B));
+  mw = 0.0f;
+}
+template <> DEV void i8_codes<FM_Q4_K>(const u8* row, u32 b, u32 h, i32x4& c, float& dw, float& mw) {
+  const u8* B = row + 144u * (b >> 3);
+  const u32 j = b & 7u;
+  const uint4 hd = *(const uint4*)B;
+  const uint4 q = *(const uint4*)(B + 16 + 32 * (j >> 1) + 16 * h);
+  const u32 sh = 4u * (j & 1u);
+  c[0] = (int)((q.x >> sh) & 0x0F0F0F0Fu);
+  c[1] = (int)((q.y >> sh) & 0x0F0F0F0Fu);
+  c[2] = (int)((q.z >> sh) & 0x0F0F0F0Fu);
+  c[3] = (int)((q.w >> sh) & 0x0F0F0F0Fu);
+  u32 sc, mn;
+  k4_scmin(hd, j, sc, mn);
+  dw = f16v(hd.x & 0xffffu) * (float)sc;
+  mw = f16v(hd.x >> 16) * (float)mn;
+}
+template <> DEV void i8_codes<FM_Q5_K>(const u8* row, u32 b, u32 h, i32x4& c, float& dw, float& mw) {
+  const u8* B = row + 176u * (b >> 3);
+  const u32 j = b & 7u;
+  const uint4 hd = *(const uint4*)B;
+  const uint4 qh = *(const uint4*)(B + 16 + 16 * h);
+  const uint4 q = *(const uint4*)(B + 48 + 32 * (j >> 1) + 16 * h);
+  const u32 sh = 4u * (j & 1u);
+  c[0] = (int)(((q.x >> sh) & 0x0F0F0F0Fu) | (((qh.x >> j) & 0x01010101u) << 4));
+  c[1] = (int)(((q.y >> sh) & 0x0F0F0F0Fu) | (((qh.y >> j) & 0x01010101u) << 4));
+  c[2] = (int)(((q.z >> sh) & 0x0F0F0F0Fu) | (((qh.z >> j) & 0x01010101u) << 4));
+  c[3] = (int)(((q.w >> sh) & 0x0F0F0F0Fu) | (((qh.w >> j) & 0x01010101u) << 4));
+  u32 sc, mn;
+  k4_scmin(hd, j, sc, mn);
+  dw = f16v(hd.x & 0xffffu) * (float)sc;
+  mw = f16v(hd.x >> 16) * (float)mn;
+}
+// Q6_K: half k (columns 16 k .. 16 k + 15) of block b, the lane's 8 columns 16 k + 8 h .. as q - 32
+// (signed bytes), and that half's scale d sc_k
+DEV void i8_q6_half(const u8* row, u32 b, u32 k, u32 h, long& c, float& ds) {
+  const u8* B = row + 210u * (b >> 3);
+  const u32 bb = b & 7u, n = bb >> 2, quad = bb & 3u, i0 = 16 * k + 8 * h;
+  const u8* pl = B + 64 * n + 32 * (quad & 1u) + i0;
+  const u8* ph = B + 128 + 32 * n + i0;
+  const u32 nsh = quad >= 2u ? 4u : 0u, hsh = 2u * quad;
+  u32 o[2];
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    const u32 lw = ld_u16(pl + 4 * t) | ld_u16(pl + 4 * t + 2) << 16;
+    const u32 hw = ld_u16(ph + 4 * t) | ld_u16(ph + 4 * t + 2) << 16;
+    const u32 v = ((lw >> nsh) & 0x0F0F0F0Fu) | (((hw >> hsh) & 0x03030303u) << 4);
+    o[t] = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;  // per byte q - 32
+  }
+  c = (long)((u64)o[0] | (u64)o[1] << 32);
+  ds = f16v(ld_u16(B + 208)) * (float)(int)(signed char)B[192 + 8 * n + 2 * quad + k];
+}
+
+
+constexpr u32 QG_CH = 32;  // blocks of {d, s} staged in LDS at a time (64 slots x 32 blocks x 8 bytes)
+
+template <u32 F, u32 MODE, u32 NL>
+DEV void gemm_i8_body(const GemmQ8Args& g, float2* lsd, u32 e, u32 base, u32 m0, u32 M, u32 ntile) {
+  const u32 tid = threadIdx.x, w = tid >> 6, l = tid & 63, h = l >> 5, lr = l & 31;
+  const u32 nb = g.K / 32;
+  const u32 live = M - m0;
+  const int8_t* arow[NL];
+#pragma unroll
+  for (u32 mf = 0; mf < NL; mf++) {
+    const u32 slot = base + m0 + min(32 * mf + lr, live - 1);  // rows past the tile repeat a live one
+    const u32 src = g.xmap ? g.xmap[slot] : slot;
+    arow[mf] = g.A + (u64)src * g.K + 16 * h;
+  }
+  const u8 *br0, *br1;
+  if (MODE == 0) {
+    const u64 f = (u64)ntile * 128 + 32 * w + lr;
+    br0 = g.W0 + (u64)e * g.es + f * g.rb;
+    br1 = g.W1 + (u64)e * g.es + f * g.rb;
+  } else {
+    const u64 n = (u64)ntile * 256 + 64 * w + lr;
+    br0 = g.W0 + (u64)e * g.es + n * g.rb;
+    br1 = br0 + 32 * g.rb;
+  }
+  float acc[NL][2][16];
+#pragma unroll
+  for (u32 mf = 0; mf < NL; mf++)
+#pragma unroll
+    for (u32 nf = 0; nf < 2; nf++)
+#pragma unroll
+      for (u32 i = 0; i < 16; i++) acc[mf][nf][i] = 0.0f;
+  const i32x16 z16 = {};
+  for (u32 c0 = 0; c0 < nb; c0 += QG_CH) {
+    const u32 cn = min(QG_CH, nb - c0);
+    __syncthreads();  // the previous chunk's readers are done
+    for (u32 i = tid; i < 64 * cn; i += 256) {
+      const u32 b = i / 64, r = i % 64;
+      const u32 slot = base + m0 + min(r, live - 1);
+      const u32 src = g.xmap ? g.xmap[slot] : slot;
+      lsd[i] = g.Ad[(u64)src * nb + c0 + b];
+    }
+    __syncthreads();
+#pragma unroll 2
+    for (u32 bi = 0; bi < cn; bi++) {
+      const u32 b = c0 + bi;
+      if constexpr (F == FM_Q6_K) {
+        long a0[NL], a1[NL], w00, w01, w10, w11;
+        float s00, s01, s10, s11;
+#pragma unroll
+        for (u32 mf = 0; mf < NL; mf++) {
+          a0[mf] = *(const long*)(arow[mf] + 32 * b - 8 * h);       // columns 8 h .. 8 h + 7
+          a1[mf] = *(const long*)(arow[mf] + 32 * b + 16 - 8 * h);  // columns 16 + 8 h ..
+        }
+        i8_q6_half(br0, b, 0, h, w00, s00);
+        i8_q6_half(br0, b, 1, h, w01, s01);
+        i8_q6_half(br1, b, 0, h, w10, s10);
+        i8_q6_half(br1, b, 1, h, w11, s11);
+#pragma unroll
+        for (u32 mf = 0; mf < NL; mf++) {
+          const i32x16 p00 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a0[mf], w00, z16, 0, 0, 0);
+          const i32x16 p01 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a1[mf], w01, z16, 0, 0, 0);
+          const i32x16 p10 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a0[mf], w10, z16, 0, 0, 0);
+          const i32x16 p11 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a1[mf], w11, z16, 0, 0, 0);
+#pragma unroll
+          for (u32 i = 0; i < 16; i++) {
+            const float dx = lsd[bi * 64 + 32 * mf + 8 * (i >> 2) + 4 * h + (i & 3)].x;
+            acc[mf][0][i] = __builtin_fmaf(dx, __builtin_fmaf(s01, (float)p01[i], s00 * (float)p00[i]), acc[mf][0][i]);
+            acc[mf][1][i] = __builtin_fmaf(dx, __builtin_fmaf(s11, (float)p11[i], s10 * (float)p10[i]), acc[mf][1][i]);
+          }
+        }
+      } else {
+        i32x4 a[NL], w0, w1;
+        float dw0, mw0, dw1, mw1;
+#pragma unroll
+        for (u32 mf = 0; mf < NL; mf++) a[mf] = *(const i32x4*)(arow[mf] + 32 * b);
+        i8_codes<F>(br0, b, h, w0, dw0, mw0);
+        i8_codes<F>(br1, b, h, w1, dw1, mw1);
+#pragma unroll
+        for (u32 mf = 0; mf < NL; mf++) {
+          const i32x16 p0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[mf], w0, z16, 0, 0, 0);
+          const i32x16 p1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[mf], w1, z16, 0, 0, 0);
+#pragma unroll
+          for (u32 i = 0; i < 16; i++) {
+            const float2 ds = lsd[bi * 64 + 32 * mf + 8 * (i >> 2) + 4 * h + (i & 3)];
+            float v0 = __builtin_fmaf(dw0 * ds.x, (float)p0[i], acc[mf][0][i]);
+            float v1 = __builtin_fmaf(dw1 * ds.x, (float)p1[i], acc[mf][1][i]);
+            if constexpr (F != FM_Q8_0) {
+              v0 = __builtin_fmaf(-mw0, ds.y, v0);
+              v1 = __builtin_fmaf(-mw1, ds.y, v1);
+            }
+            acc[mf][0][i] = v0;
+            acc[mf][1][i] = v1;
+          }
+        }
+      }
+    }
+  }
+  // epilogue: acc[mf][b][i] is slot row 32 mf + 8 (i / 4) + 4 h + i % 4 of the tile, weight row lr of
+  // the wave's row block b
+#pragma unroll
+  for (u32 mf = 0; mf < NL; mf++)
+#pragma unroll
+    for (u32 i = 0; i < 16; i++) {
+      const u32 row = 32 * mf + 8 * (i >> 2) + 4 * h + (i & 3);
+      if (m0 + row >= M) continue;
+      const u64 s = base + m0 + row;
+      if (MODE == 0) {
+        g.out[s * g.N + ntile * 128 + 32 * w + lr] = silu_mul(acc[mf][0][i], acc[mf][1][i]);
+      } else {
+#pragma unroll
+        for (u32 b = 0; b < 2; b++) g.out[s * g.N + ntile * 256 + 64 * w + 32 * b + lr] = acc[mf][b][i];
+      }
+    }
+}
+
+template <u32 F, u32 MODE>
+__global__ void __launch_bounds__(256, 2) k_gemm_i8(GemmQ8Args g, u32 NT) {
+  __shared__ float2 lsd[64 * QG_CH];
+  const u32 q = blockIdx.x >> 3, ntile = q % NT, L = threadIdx.x & 63;
+  u32 te[G3_NEC];
+  u32 ntl;
+  if (g.off) {
+    tiles_load(g.off, g.ne, L, te);
+    ntl = __builtin_amdgcn_readfirstlane(tiles_total(te, g.ne));
+  } else {
+    ntl = (g.M + G3_BM - 1) / G3_BM;
+  }
+  const u32 C = (ntl + 7) / 8;
+  const u32 tile = (blockIdx.x & 7) * C + q / NT;
+  if (q / NT >= C || tile >= ntl) return;
+  u32 e, m0, base, M;
+  if (g.off) {
+    u32 k;
+    tiles_find(te, g.ne, tile, L, e, k);
+    e = __builtin_amdgcn_readfirstlane(e);
+    m0 = __builtin_amdgcn_readfirstlane(k) * G3_BM;
+    base = g.off[e];
+    M = g.off[e + 1] - base;
+  } else {
+    e = 0;
+    m0 = tile * G3_BM;
+    base = 0;
+    M = g.M;
+  }
+  if (M - m0 <= 32) gemm_i8_body<F, MODE, 1>(g, lsd, e, base, m0, M, ntile);
+  else gemm_i8_body<F, MODE, 2>(g, lsd, e, base, m0, M, ntile);
+}
+
+int launch_gemm_i8(const GemmQ8Args& g, u32 fm, u32 mode, u32 grid_y, hipStream_t st) {
+  const u32 nf = mode == 0 ? 128u : 256u;
+  if (g.K % 32 || g.N % nf || fm == FM_F32) return -1;
+  if ((fm != FM_Q8_0 && g.K % 256) || (g.off && (g.ne == 0 || g.ne > 64 * G3_NEC))) return -1;
+  const u32 NT = g.N / nf;
+  const dim3 grid(8 * NT * ((grid_y + 7) / 8));
+#define GI_L(F) \
+  if (fm == F) { \
+    if (mode == 0) LAUNCH_K((k_gemm_i8<F, 0>), grid, dim3(256), 0, st, g, NT); \
+    else LAUNCH_K((k_gemm_i8<F, 1>), grid, dim3(256), 0, st, g, NT); \
+    return 0; \
+  }
+  GI_L(FM_Q8_0) GI_L(FM_Q4_K) GI_L(FM_Q5_K) GI_L(FM_Q6_K)
+#undef GI_L
+  return -1;
 }
 
 // ---------------------------------------------------------------- launchers
@@ -569,8 +828,15 @@ int launch_pack(u32 fm, const u8* W, u64 es, u64 rb, u32 R, u32 K, u32 ne, u8* P
 int launch_combine(const _Float16* out, const float* spill, const u32* inv, const float* wt, u32 nk, const float* shd,
                    const float* sgo, const float* x1, float* y, u32 dm, u32 T, hipStream_t st) {
   if (dm % 4 || nk > 64 || !spill) return -1;
-  hipLaunchKernelGGL(k_combine, dim3((dm / 4 + 255) / 256, T), dim3(256), 0, st, out, spill, inv, wt, nk, shd, sgo, x1,
-                     y, dm);
+  hipLaunchKernelGGL(k_combine<_Float16>, dim3((dm / 4 + 255) / 256, T), dim3(256), 0, st, out, spill, inv, wt, nk, shd,
+                     sgo, x1, y, dm);
+  return 0;
+}
+int launch_combine_f32(const float* out, const u32* inv, const float* wt, u32 nk, const float* shd, const float* sgo,
+                       const float* x1, float* y, u32 dm, u32 T, hipStream_t st) {
+  if (dm % 4 || nk > 64) return -1;
+  hipLaunchKernelGGL(k_combine<float>, dim3((dm / 4 + 255) / 256, T), dim3(256), 0, st, out, nullptr, inv, wt, nk, shd,
+                     sgo, x1, y, dm);
   return 0;
 }
 u32 gemm_bm() { return GM_BM; }

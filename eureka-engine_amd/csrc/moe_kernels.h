@@ -188,6 +188,25 @@ struct GemmArgs {
   uint64_t pes;       // packed expert stride
 };
 int launch_moe_gemm(const GemmArgs& g, uint32_t fm, uint32_t mode, uint32_t grid_y, hipStream_t st);
+// the q8 tier's grouped GEMM on int8 MFMA (many tokens): q8_1 activations against the GGUF codes
+struct GemmQ8Args {
+  const uint8_t* W0;   // GGUF rows: gate (mode 0) or the one matrix (mode 1)
+  const uint8_t* W1;   // up rows (mode 0)
+  uint64_t es, rb;     // expert stride, row bytes
+  uint32_t K, N, M;    // columns (K % 32 == 0), weight rows (mode 0: features), rows when off is null
+  const int8_t* A;     // q8_1 codes, rows of K
+  const float2* Ad;    // {d, s} a row's 32-column block
+  const uint32_t* xmap;  // slot -> A row, or null: the slot itself
+  const uint32_t* off;   // [ne + 1] slot offsets, or null (M rows, no experts: the shared expert)
+  uint32_t ne;
+  float* out;          // mode 0: SwiGLU [slots][N]; mode 1: [slots][N]
+};
+int launch_gemm_i8(const GemmQ8Args& g, uint32_t fm, uint32_t mode, uint32_t grid_y, hipStream_t st);
+int launch_combine_f32(const float* out, const uint32_t* inv, const float* wt, uint32_t nk, const float* shd,
+                       const float* sgo, const float* x1, float* y, uint32_t dm, uint32_t T, hipStream_t st);
+int launch_group(const uint32_t* ids, uint32_t n, uint32_t nk, uint32_t ne, uint32_t* off, uint32_t* xmap,
+                 uint32_t* inv, const float* x, _Float16* x16, uint64_t nx, hipStream_t st);
+int launch_q8_1(const float* x, uint32_t n, int8_t* q, float2* ds, hipStream_t st);
 uint32_t gemm_bm();
 int llb_fail_msg(int code, const char* msg);  // sets llb_hip_last_error's text, returns code
 // the static scratch's device address on the current device, resolved once (moe_noalloc.hip)

@@ -3,6 +3,8 @@
 // dot is an int8 dot product (v_dot4_i32_i8) scaled in f32: Q4_K / Q5_K (d sc) xd acc - (dmin m) xs,
 // Q6_K d xd (sc0 a0 + sc1 a1), Q8_0 d xd acc. Routing stays the exact tier's. Tolerance class.
 // Also the dispatch permutation (llb_mx_group) and the q8_1 quantizer (pf_q8x).
+#include <stdlib.h>
+
 #include "../../include/llb_moe_hip.h"
 #include "moe_dev.h"
 #include "moe_kernels.h"
@@ -203,10 +205,144 @@ static uint64_t rbytes(uint32_t fm, uint32_t cols) {
        : fm == FM_Q6_K ? (uint64_t)cols / 256 * 210 : fm == FM_Q5_K ? (uint64_t)cols / 256 * 176 : 0;
 }
 
+// many tokens: the grouped GEMM path on int8 MFMA (moe_q8_gemm below)
+#define Q8_GEMM_T 16u
+struct Q8GemmLayout {
+  size_t hq, hd, off, xmap, inv, act, aq, ad, out, sa, sq, sd, shd, total;
+};
+static Q8GemmLayout q8_gemm_layout(const llb_moe_layer* L, uint32_t T) {
+  Q8GemmLayout g;
+  const size_t n = (size_t)T * L->nk;
+  size_t o = 0;
+  g.hq = o; o += al((size_t)T * L->dm);
+  g.hd = o; o += al((size_t)T * L->dm / 32 * 8);
+  g.off = o; o += al(((size_t)L->ne + 1) * 4);
+  g.xmap = o; o += al(n * 4);
+  g.inv = o; o += al(n * 4);
+  g.act = o; o += al(n * L->ef * 4);
+  g.aq = o; o += al(n * L->ef);
+  g.ad = o; o += al(n * L->ef / 32 * 8);
+  g.out = o; o += al(n * L->dm * 4);
+  g.sa = o; o += al((size_t)T * L->sf * 4 + 4);
+  g.sq = o; o += al((size_t)T * L->sf + 4);
+  g.sd = o; o += al((size_t)T * L->sf / 32 * 8 + 8);
+  g.shd = o; o += al((size_t)T * L->dm * 4);
+  g.total = o;
+  return g;
+}
+// The int8-MFMA path is switched on by LLB_MOE_Q8_GEMM=1 (read once). It is off by default until it has
+// run on the GPU: its first run faulted (its Q8_0 code loads read 4 bytes past the stack's last block,
+// fixed since), and the fixed code has not run yet. Off, the q8 tier keeps its per-slot kernels at
+// every T.
+static bool q8_gemm_on() {
+  static const int on = [] {
+    const char* e = getenv("LLB_MOE_Q8_GEMM");
+    return e && e[0] == '1' ? 1 : 0;
+  }();
+  return on != 0;
+}
+static bool q8_gemm_ok(const llb_moe_layer* L, uint32_t T) {
+  const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15;
+  return q8_gemm_on() && T >= Q8_GEMM_T && fg == fu && (!L->sf || L->fsg == L->fsu) && L->ef % 128 == 0 && L->sf % 128 == 0 &&
+         L->dm % 256 == 0 && L->ne <= 1024;
+}
 size_t moe_q8_scratch(const llb_moe_layer* L, uint32_t T) {
   const size_t n = (size_t)T * L->nk;
-  return al((size_t)T * L->dm) + al((size_t)T * L->dm / 32 * 8) + al(n * L->ef * 4) + al(n * L->ef) +
-         al(n * L->ef / 32 * 8) + al((size_t)T * L->sf * 4 + 4) + al((size_t)T * L->sf + 4) + al((size_t)T * L->sf / 32 * 8 + 8);
+  const size_t gemv = al((size_t)T * L->dm) + al((size_t)T * L->dm / 32 * 8) + al(n * L->ef * 4) + al(n * L->ef) +
+                      al(n * L->ef / 32 * 8) + al((size_t)T * L->sf * 4 + 4) + al((size_t)T * L->sf + 4) +
+                      al((size_t)T * L->sf / 32 * 8 + 8);
+  const size_t gm = q8_gemm_ok(L, T) ? q8_gemm_layout(L, T).total : 0;
+  return gemv > gm ? gemv : gm;
+}
+
+// the q8 tier for many tokens: x to q8_1; the slots grouped by expert; the gate / up GEMM (int8 MFMA,
+// SwiGLU in the epilogue); act to q8_1; the down GEMM; the shared expert as one more "expert" over the T
+// tokens; the rank-order combine with the shared gate and the residual
+static int moe_q8_gemm(const llb_moe_layer* L, uint32_t T, const float* h2, const float* x1, float* y,
+                       const uint32_t* ids, const float* wt, const float* sgo, uint8_t* sc, hipStream_t st) {
+  const Q8GemmLayout q = q8_gemm_layout(L, T);
+  const uint32_t fg = L->fx & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
+  const uint32_t n = T * L->nk;
+  int8_t* hq = (int8_t*)(sc + q.hq);
+  float2* hd = (float2*)(sc + q.hd);
+  uint32_t* off = (uint32_t*)(sc + q.off);
+  uint32_t* xmap = (uint32_t*)(sc + q.xmap);
+  uint32_t* inv = (uint32_t*)(sc + q.inv);
+  float* act = (float*)(sc + q.act);
+  int8_t* aq = (int8_t*)(sc + q.aq);
+  float2* ad = (float2*)(sc + q.ad);
+  float* out = (float*)(sc + q.out);
+  const uint64_t rbg = rbytes(fg, L->dm), rbd = rbytes(fd, L->ef);
+  stage_begin(ST_Q8X);
+  int rc = launch_q8_1(h2, T * L->dm, hq, hd, st);
+  if (!rc) rc = launch_group(ids, n, L->nk, L->ne, off, xmap, inv, nullptr, nullptr, 0, st);
+  stage_end(ST_Q8X);
+  if (rc) return rc;
+  const uint32_t maxt = n / gemm_bm() + L->ne + 1;  // >= sum over experts of ceil(M_e / 64)
+  GemmQ8Args g{};
+  g.W0 = (const uint8_t*)(uintptr_t)L->G;
+  g.W1 = fz ? g.W0 + (uint64_t)L->ef * rbg : (const uint8_t*)(uintptr_t)L->U;
+  g.es = (uint64_t)(fz ? 2 : 1) * L->ef * rbg;
+  g.rb = rbg;
+  g.K = L->dm;
+  g.N = L->ef;
+  g.A = hq;
+  g.Ad = hd;
+  g.xmap = xmap;
+  g.off = off;
+  g.ne = L->ne;
+  g.out = act;
+  stage_begin(ST_GU);
+  rc = launch_gemm_i8(g, fg, 0, maxt, st);
+  stage_end(ST_GU);
+  if (rc) return rc;
+  if ((rc = launch_q8_1(act, n * L->ef, aq, ad, st))) return rc;
+  GemmQ8Args d{};
+  d.W0 = (const uint8_t*)(uintptr_t)L->D;
+  d.es = (uint64_t)L->dm * rbd;
+  d.rb = rbd;
+  d.K = L->ef;
+  d.N = L->dm;
+  d.A = aq;
+  d.Ad = ad;
+  d.off = off;
+  d.ne = L->ne;
+  d.out = out;
+  stage_begin(ST_DN);
+  rc = launch_gemm_i8(d, fd, 1, maxt, st);
+  stage_end(ST_DN);
+  if (rc) return rc;
+  const float* shd = nullptr;
+  if (L->sf) {
+    float* sa = (float*)(sc + q.sa);
+    int8_t* sq = (int8_t*)(sc + q.sq);
+    float2* sd = (float2*)(sc + q.sd);
+    const uint32_t mt = (T + gemm_bm() - 1) / gemm_bm();
+    GemmQ8Args s{};
+    s.W0 = (const uint8_t*)(uintptr_t)L->SG;
+    s.W1 = (const uint8_t*)(uintptr_t)L->SU;
+    s.rb = rbytes(L->fsg, L->dm);
+    s.K = L->dm;
+    s.N = L->sf;
+    s.M = T;
+    s.A = hq;
+    s.Ad = hd;
+    s.out = sa;
+    if ((rc = launch_gemm_i8(s, L->fsg, 0, mt, st))) return rc;
+    if ((rc = launch_q8_1(sa, T * L->sf, sq, sd, st))) return rc;
+    GemmQ8Args sd2{};
+    sd2.W0 = (const uint8_t*)(uintptr_t)L->SD;
+    sd2.rb = rbytes(L->fsd, L->sf);
+    sd2.K = L->sf;
+    sd2.N = L->dm;
+    sd2.M = T;
+    sd2.A = sq;
+    sd2.Ad = sd;
+    sd2.out = (float*)(sc + q.shd);
+    if ((rc = launch_gemm_i8(sd2, L->fsd, 1, mt, st))) return rc;
+    shd = sd2.out;
+  }
+  return launch_combine_f32(out, inv, wt, L->nk, shd, sgo, x1, y, L->dm, T, st);
 }
 
 // few tokens: each kernel quantizes the activations it reads in LDS (no q8_1 launches); more: the
@@ -215,6 +351,7 @@ size_t moe_q8_scratch(const llb_moe_layer* L, uint32_t T) {
 
 int moe_q8_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const float* x1, float* y, const uint32_t* ids,
                    const float* wt, const float* sgo, const TopkArgs* tk, uint8_t* sc, hipStream_t st) {
+  if (!tk && q8_gemm_ok(L, T)) return moe_q8_gemm(L, T, h2, x1, y, ids, wt, sgo, sc, st);
   const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15, fd = L->fx >> 8 & 15, fz = L->fx >> 12 & 1;
   Q8Args a{};
   const size_t n = (size_t)T * L->nk;

@@ -103,3 +103,63 @@ def test_group_chunks_in_range(n):
                 else:
                     assert all(j < n for j in range(i, i1))  # the ragged tail: words below i1 only
     assert covered == list(range(n))                      # every slot once, in slot order
+
+
+# the q8 tier's int8 GEMM decoders (eureka-engine_amd/csrc/moe_gemm.hip): i8_codes<F>(row, b, h) and
+# i8_q6_half(row, b, k, h), restated
+def i8_reads(fm, b, h):
+    if fm == 1:
+        B = 34 * b
+        p = B + 2 + 16 * h
+        rng = [(B, B + 2)]
+        if p % 4 == 0:
+            return rng + [(p, p + 16)]
+        return rng + [(p, p + 2), (p + 2, p + 14), (p + 14, p + 16)]
+    j = b & 7
+    if fm == 3:
+        B = 144 * (b >> 3)
+        q = B + 16 + 32 * (j >> 1) + 16 * h
+        return [(B, B + 16), (q, q + 16)]
+    if fm == 9:
+        B = 176 * (b >> 3)
+        q = B + 48 + 32 * (j >> 1) + 16 * h
+        return [(B, B + 16), (B + 16 + 16 * h, B + 32 + 16 * h), (q, q + 16)]
+    raise ValueError(fm)
+
+
+def i8_q6_reads(b, k, h):
+    B = 210 * (b >> 3)
+    bb = b & 7
+    n, quad = bb >> 2, bb & 3
+    i0 = 16 * k + 8 * h
+    pl, ph = B + 64 * n + 32 * (quad & 1) + i0, B + 128 + 32 * n + i0
+    sc = B + 192 + 8 * n + 2 * quad + k
+    return [(pl, pl + 8), (ph, ph + 8), (B + 208, B + 210), (sc, sc + 1)]
+
+
+@pytest.mark.parametrize("fm,cols", [(1, 32), (1, 64), (1, 768), (1, 2048), (3, 256), (3, 2048), (9, 512)])
+def test_int8_gemm_codes_stay_inside_the_row(fm, cols):
+    b_, n = BLK[fm]
+    rb = cols // n * b_
+    for b in range(cols // 32):
+        for h in (0, 1):
+            for s, e in i8_reads(fm, b, h):
+                assert 0 <= s <= e <= rb, (fm, cols, b, h, s, e, rb)
+
+
+def test_five_dword_q8_0_window_would_read_past_the_row():
+    """the control: five aligned dwords from the code span (the loads this decoder had) end 4 bytes past
+    the last block of a 2048-column Q8_0 row, so the checks above can see that mistake"""
+    rb, B = 2176, 34 * 63
+    p = B + 2 + 16
+    assert p % 4 == 0 and p - (p & 3) + 20 > rb
+
+
+@pytest.mark.parametrize("cols", [256, 512, 2048])
+def test_int8_gemm_q6_halves_stay_inside_the_row(cols):
+    rb = cols // 256 * 210
+    for b in range(cols // 32):
+        for k in (0, 1):
+            for h in (0, 1):
+                for s, e in i8_q6_reads(b, k, h):
+                    assert 0 <= s < e <= rb, (cols, b, k, h, s, e, rb)

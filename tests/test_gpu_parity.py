@@ -334,7 +334,8 @@ def test_q8_1_matches_oracle(dev):
     assert np.array_equal(gds[:, 1], rs)  # s: the same xor-butterfly order
 
 
-@pytest.mark.parametrize("name,T", [("c2", 1), ("c1", 4), ("c2", 8), ("c1", 16)])
+# T >= 16: the grouped GEMM on int8 MFMA (c2 / c5: with the shared expert; c1k: Q4_K gate / up, Q6_K down)
+@pytest.mark.parametrize("name,T", [("c2", 1), ("c1", 4), ("c2", 8), ("c1", 16), ("c2", 40), ("c1k", 100), ("c5", 70)])
 def test_q8_tier_tolerance(dev, name, T):
     shape = em.SHAPES[name]
     _say("q8", name, T)
@@ -355,6 +356,29 @@ def test_q8_tier_tolerance(dev, name, T):
     m64 = ol.err_metrics(y, hl.f64(h2, ids))
     _say("q8 vs float64", m64)
     assert m64["cos"] >= 0.999
+
+
+@pytest.mark.parametrize("name", ["c1", "c1k"])
+def test_q8_tier_prefill_2048_sampled(dev, name):
+    """config 4 on the q8 tier (the int8-MFMA grouped GEMM): 2048 tokens, 64 sampled tokens (the first and
+    last tiles of the most-loaded expert among them) against the oracle's q8 mode"""
+    shape, T, seed = em.SHAPES[name], 2048, 6
+    _say("q8 prefill", name, "T", T)
+    layer = em.Layer(dev, shape, seed=seed)
+    run = em.Runner(dev, shape, T, tier=em.Q8)
+    run.gen_inputs(seed)
+    run.forward(layer, residual=False)
+    y, ids, wt = run.outputs()
+    run.free()
+    layer.free()
+    toks, big, mine = _sample_tokens(ids, T, seed)
+    h2, _ = ol.inputs(shape, seed, T)
+    yq, idq, wtq, _ = ol.HostLayer(shape, seed=seed, experts=[]).run(h2[toks], None, tier="q8",
+                                                                    nthreads=ORACLE_THREADS)
+    assert np.array_equal(ids[toks], idq) and np.array_equal(wt[toks].view(np.uint32), wtq.view(np.uint32))
+    m = ol.err_metrics(y[toks], yq)
+    _say("q8 prefill vs oracle q8", m)
+    assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
 
 
 def test_q8_tier_same_bits_every_path(dev):
