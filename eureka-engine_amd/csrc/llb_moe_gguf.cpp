@@ -17,6 +17,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <condition_variable>
 #include <cstdio>
 #include <cstdlib>
@@ -45,7 +46,14 @@ struct llb_gguf {
   uint64_t size;
   uint32_t version, alignment;
   std::vector<GgTensor> t;
+  std::string arch;                                   // general.architecture
+  std::vector<std::pair<std::string, int64_t>> ints;  // scalar integer metadata, by key
 };
+static bool gg_int(const llb_gguf* g, const std::string& key, int64_t* v) {
+  for (const auto& kv : g->ints)
+    if (kv.first == key) return (*v = kv.second, true);
+  return false;
+}
 
 // ggml type -> (block bytes, block elements); 0 for types this path does not read
 static bool gg_block(uint32_t ty, uint64_t& bb, uint64_t& be) {
@@ -141,6 +149,8 @@ llb_gguf* llb_gguf_open(const char* path) {
   else if (version < 2 || version > 3) why = "gguf: only versions 2 and 3";
   else if (nt > (1u << 24) || nkv > (1u << 24)) why = "gguf: implausible tensor or key count";
   uint32_t alignment = 32;
+  std::string arch;
+  std::vector<std::pair<std::string, int64_t>> ints;
   for (uint64_t i = 0; !why && i < nkv; i++) {
     std::string key;
     r.str(&key);
@@ -148,12 +158,27 @@ llb_gguf* llb_gguf_open(const char* path) {
     if (key == "general.alignment" && ty == 4) {
       alignment = r.v<uint32_t>();
       if (alignment == 0 || (alignment & (alignment - 1))) why = "gguf: general.alignment not a power of two";
+    } else if (key == "general.architecture" && ty == 8) {
+      r.str(&arch);
+    } else if (ty <= 5 || ty == 10 || ty == 11) {  // scalar integers, kept by key
+      int64_t v = 0;
+      switch (ty) {
+        case 0: v = r.v<uint8_t>(); break;
+        case 1: v = r.v<int8_t>(); break;
+        case 2: v = r.v<uint16_t>(); break;
+        case 3: v = r.v<int16_t>(); break;
+        case 4: v = r.v<uint32_t>(); break;
+        case 5: v = r.v<int32_t>(); break;
+        case 10: v = (int64_t)r.v<uint64_t>(); break;
+        default: v = r.v<int64_t>(); break;
+      }
+      ints.emplace_back(key, v);
     } else {
       r.skip(ty);
     }
     if (r.bad) why = "gguf: truncated or malformed metadata";
   }
-  auto* g = new llb_gguf{fd, (uint64_t)st.st_size, version, alignment, {}};
+  auto* g = new llb_gguf{fd, (uint64_t)st.st_size, version, alignment, {}, arch, ints};
   if (!why) g->t.reserve((size_t)nt);
   for (uint64_t i = 0; !why && i < nt; i++) {
     GgTensor t{};
@@ -220,6 +245,135 @@ int llb_gguf_tensor_at(const llb_gguf* g, uint64_t i, char* name, size_t cap, ui
   if (nd) *nd = t.nd;
   if (dims)
     for (uint32_t d = 0; d < 4; d++) dims[d] = d < t.nd ? t.dims[d] : 1;
+  return 0;
+}
+
+// table.bin rows from the GGUF header (the reference's sidecar writer, tools/gguf2pack.c:1134-1346 for
+// qwen35moe): the virtual pack layout is the non-layer tensors, then each layer's trunk (every tensor but
+// the *_exps stacks), file order within each, then every *_exps stack in layer order, each at a 64-byte
+// boundary. A row's word 0 is its layer's trunk bytes; words 1..20 the dense tensors' offsets in the trunk
+// (| format << 28), the shared expert under the dense ffn names (words 3..5); 21 the router, 22 the shared
+// gate row; 26 the expert formats (gate | up << 4 | down << 8, bit 12 fused gate+up, bit 13); 27 experts,
+// 28 expert ff, 29 shared ff, 30 experts used. The nextn (MTP) blocks at the end are left out.
+static int gg_fm_any(uint32_t ty) {
+  switch (ty) {
+    case 0: return 0;   // F32
+    case 1: return 2;   // F16
+    case 8: return 1;   // Q8_0
+    case 12: return 3;  // Q4_K
+    case 13: return 9;  // Q5_K
+    case 14: return 4;  // Q6_K
+    default: return -1;
+  }
+}
+static int gg_layer(const std::string& n) {
+  if (n.compare(0, 4, "blk.") != 0) return -1;
+  int L = 0;
+  size_t i = 4;
+  if (i >= n.size() || n[i] < '0' || n[i] > '9') return -1;
+  while (i < n.size() && n[i] >= '0' && n[i] <= '9' && L < (1 << 20)) L = 10 * L + (n[i++] - '0');
+  return i < n.size() && n[i] == '.' ? L : -1;
+}
+static bool gg_exps(const std::string& n) { return n.size() > 12 && n.compare(n.size() - 12, 12, "_exps.weight") == 0; }
+
+int llb_moe_table_from_gguf(const llb_gguf* g, uint32_t* table, uint32_t cap, uint32_t* nlayers) {
+  static const char* offs[20] = {
+      "attn_norm.weight", "post_attention_norm.weight", "ffn_gate.weight", "ffn_up.weight", "ffn_down.weight",
+      "attn_qkv.weight", "attn_gate.weight", "ssm_beta.weight", "ssm_alpha.weight", "ssm_a", "ssm_dt.bias",
+      "ssm_conv1d.weight", "ssm_norm.weight", "ssm_out.weight", "attn_q.weight", "attn_k.weight", "attn_v.weight",
+      "attn_q_norm.weight", "attn_k_norm.weight", "attn_output.weight"};
+  static const char* shn[3] = {"ffn_gate_shexp.weight", "ffn_up_shexp.weight", "ffn_down_shexp.weight"};
+  if (!g || !nlayers) return llb_fail_msg(LLB_HIP_EINVAL, "table: null file or count");
+  if (g->arch != "qwen35moe") return llb_fail_msg(LLB_HIP_EINVAL, "table: general.architecture is not qwen35moe");
+  int64_t L0 = 0, ne = 0, nk = 0, ef = 0, sf = 0, mtp = 0;
+  const std::string a = g->arch + ".";
+  if (!gg_int(g, a + "block_count", &L0) || !gg_int(g, a + "expert_count", &ne) ||
+      !gg_int(g, a + "expert_used_count", &nk) || !gg_int(g, a + "expert_feed_forward_length", &ef) ||
+      !gg_int(g, a + "expert_shared_feed_forward_length", &sf))
+    return llb_fail_msg(LLB_HIP_EINVAL, "table: a qwen35moe expert / block count key is missing");
+  gg_int(g, a + "nextn_predict_layers", &mtp);
+  if (L0 < 1 || L0 > 4096 || ne < 1 || ne > 0xffffffffll || nk < 1 || nk > ne || ef < 1 || sf < 1 || mtp < 0 ||
+      mtp >= L0)
+    return llb_fail_msg(LLB_HIP_EINVAL, "table: implausible block / expert counts");
+  const uint32_t nl = (uint32_t)(L0 - mtp);
+  *nlayers = nl;
+  if (!table || cap < nl) return llb_fail_msg(LLB_HIP_EINVAL, "table: the table holds fewer rows than layers");
+  // the virtual layout: a stable order by (routed stack, layer), every tensor at a 64-byte boundary
+  const size_t n = g->t.size();
+  std::vector<size_t> ord(n);
+  std::vector<int> lay(n);
+  std::vector<char> ex(n);
+  for (size_t i = 0; i < n; i++) {
+    ord[i] = i;
+    lay[i] = gg_layer(g->t[i].name);
+    ex[i] = lay[i] >= 0 && gg_exps(g->t[i].name);
+    if (!g->t[i].bytes || gg_fm_any(g->t[i].type) < 0)
+      return llb_fail_msg(LLB_HIP_EINVAL, ("table: " + g->t[i].name + ": a tensor type the table cannot place").c_str());
+  }
+  std::stable_sort(ord.begin(), ord.end(), [&](size_t x, size_t y) {
+    return ex[x] != ex[y] ? ex[x] < ex[y] : lay[x] < lay[y];
+  });
+  std::vector<uint64_t> pos(n);
+  uint64_t at = 0;
+  for (size_t k = 0; k < n; k++) {
+    at = (at + 63) / 64 * 64;
+    pos[ord[k]] = at;
+    at += g->t[ord[k]].bytes;
+  }
+  std::vector<uint64_t> lo(nl, UINT64_MAX), hi(nl, 0);
+  for (size_t i = 0; i < n; i++)
+    if (lay[i] >= 0 && (uint32_t)lay[i] < nl && !ex[i]) {
+      lo[lay[i]] = std::min(lo[lay[i]], pos[i]);
+      hi[lay[i]] = std::max(hi[lay[i]], pos[i] + g->t[i].bytes);
+    }
+  memset(table, 0, (size_t)nl * 128);
+  for (uint32_t L = 0; L < nl; L++) {
+    if (lo[L] == UINT64_MAX) return llb_fail_msg(LLB_HIP_EINVAL, "table: a layer without trunk tensors");
+    if (hi[L] - lo[L] > (1ull << 31)) return llb_fail_msg(LLB_HIP_EINVAL, "table: a layer's trunk is over 2 GiB");
+    table[L * 32] = (uint32_t)(hi[L] - lo[L]);
+  }
+  std::vector<uint8_t> need((size_t)nl * 6, 0);  // router, shared gate row, gate, up, gate+up, down
+  for (size_t i = 0; i < n; i++) {
+    if (lay[i] < 0 || (uint32_t)lay[i] >= nl) continue;
+    const uint32_t L = (uint32_t)lay[i];
+    const std::string& nm = g->t[i].name;
+    const std::string s = nm.substr(nm.find('.', 4) + 1);
+    uint32_t* w = table + L * 32;
+    const uint32_t fm = (uint32_t)gg_fm_any(g->t[i].type);
+    int j = 0;
+    while (j < 20 && s != offs[j]) j++;
+    for (int k = 0; k < 3 && j == 20; k++)
+      if (s == shn[k]) j = 2 + k;
+    const bool router = s == "ffn_gate_inp.weight", shgate = s == "ffn_gate_inp_shexp.weight";
+    if (j < 20 || router || shgate) {
+      if (j == 20) j = router ? 20 : 21;
+      const uint64_t rel = pos[i] - lo[L];
+      if (rel >= (1ull << 28)) return llb_fail_msg(LLB_HIP_EINVAL, "table: an offset in a layer at or past 2^28");
+      w[1 + j] = (uint32_t)rel | fm << 28;
+      if (router) need[L * 6 + 0] = 1;
+      if (shgate) need[L * 6 + 1] = 1;
+      continue;
+    }
+    const int x = s == "ffn_gate_exps.weight" || s == "ffn_gate_up_exps.weight" ? 0
+                  : s == "ffn_up_exps.weight"                                 ? 1
+                  : s == "ffn_down_exps.weight"                               ? 2
+                                                                              : -1;
+    if (x < 0) return llb_fail_msg(LLB_HIP_EINVAL, ("table: " + nm + ": a tensor outside the MoE table").c_str());
+    const bool fz = s == "ffn_gate_up_exps.weight";
+    need[L * 6 + (fz ? 4 : x == 0 ? 2 : x == 1 ? 3 : 5)] = 1;
+    w[26] |= fm << (4 * x) | (fz ? 1u << 12 : 0u) | 1u << 13;
+  }
+  for (uint32_t L = 0; L < nl; L++) {
+    const uint8_t* r = &need[L * 6];
+    if (!r[0] || !r[1] || !r[5] || (!r[4] && (!r[2] || !r[3])) || (r[4] && (r[2] || r[3])))
+      return llb_fail_msg(LLB_HIP_EINVAL, "table: a layer without its router, shared gate or expert stacks");
+    uint32_t* w = table + L * 32;
+    if (w[26] >> 12 & 1) w[26] |= (w[26] & 15) << 4;  // fused: up has gate's format
+    w[27] = (uint32_t)ne;
+    w[28] = (uint32_t)ef;
+    w[29] = (uint32_t)sf;
+    w[30] = (uint32_t)nk;
+  }
   return 0;
 }
 

@@ -89,6 +89,7 @@ _SIGS = {
                                      C.POINTER(C.c_uint64)]),
     "llb_moe_hip_load_layer": (C.c_int, [C.c_void_p, C.c_uint32, C.c_int, C.POINTER(MoeLayer)]),
     "llb_moe_hip_unload_layer": (C.c_int, [C.POINTER(MoeLayer)]),
+    "llb_moe_table_from_gguf": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint32), C.c_uint32, C.POINTER(C.c_uint32)]),
     "llb_moe_hip_residency": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint32), C.POINTER(MoeLayer), C.c_uint32,
                                         C.POINTER(C.c_int), C.POINTER(C.c_uint64)]),
     "llb_moe_hip_pack": (C.c_int, [C.POINTER(MoeLayer), C.c_uint64, C.c_size_t]),

@@ -173,6 +173,13 @@ int llb_gguf_find(const llb_gguf* g, const char* name);
 int llb_gguf_tensor_at(const llb_gguf* g, uint64_t i, char* name, size_t cap, uint64_t* offset, uint64_t* bytes,
                        uint32_t* type, uint32_t* nd, uint64_t* dims);
 int llb_moe_hip_load_layer(llb_gguf* g, uint32_t layer, int mode, llb_moe_layer* L);
+/* The table rows a qwen35moe GGUF's header implies, as the reference's sidecar writer makes them
+ * (tools/gguf2pack.c:1134-1346; word map :1142-1146): word 0 the layer's trunk bytes, words 1..20 the dense
+ * tensors' offsets in the trunk (the shared expert under ffn_gate / up / down), 21 router, 22 shared gate
+ * row (offset | format << 28), 26 expert formats (bit 12 fused gate+up, bit 13 set), 27 experts, 28 expert
+ * ff, 29 shared ff, 30 experts used. table holds cap rows of 32 words; *nlayers gets the layer count (the
+ * trailing nextn blocks left out). The rows decode with llb_moe_layer_from_table. */
+int llb_moe_table_from_gguf(const llb_gguf* g, uint32_t* table, uint32_t cap, uint32_t* nlayers);
 int llb_moe_hip_unload_layer(llb_moe_layer* L);
 /* llb_moe_load's residency choice (host/llb_host.c:532-545): sums the routed stacks of the n layers
  * (layers[i] is L[i]'s block index; each stack checked as load_layer checks it) and picks DEVICE when they

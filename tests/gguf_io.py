@@ -35,7 +35,9 @@ def write(path, tensors, alignment=32, extra_kv=()):
     """tensors: [(name, ggml_type, dims (ne0 fastest), bytes)]; returns {name: absolute offset}"""
     kvs = [("general.architecture", 8, "qwen35moe"), ("general.alignment", 4, alignment),
            ("tokenizer.ggml.tokens", 9, (8, ["a", "bb", "ccc"])), ("qwen35moe.expert_count", 4, 8),
-           ("qwen35moe.rope.freq_base", 6, 1e6), ("general.tags", 9, (4, [1, 2, 3]))] + list(extra_kv)
+           ("qwen35moe.rope.freq_base", 6, 1e6), ("general.tags", 9, (4, [1, 2, 3]))]
+    extra = list(extra_kv)
+    kvs = [k for k in kvs if k[0] not in {e[0] for e in extra}] + extra  # extra_kv replaces a default key
     head = b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(kvs))
     for k in kvs:
         head += _kv(*k)
