@@ -133,7 +133,7 @@ MFMA_F16_PEAK_TFS = 2500.0
 MFMA_I8_PEAK_TOPS = 5000.0
 
 
-def prefill(dev, shape, T, layers, steps, warmup, name="", tier=None):
+def prefill(dev, shape, T, layers, steps, warmup, name="", tier=None, graph=False):
     """T-token chunks through `layers` resident layers on the f16 MFMA tier (stacks packed once,
     outside the timer) or the q8 tier: tokens/s, and the gate/up kernel's rate (algorithmic flops
     2 T nk dm ef x 2 per launch over its HIP-event time) against the f16 MFMA peak (f16 tier) or the
@@ -146,16 +146,35 @@ def prefill(dev, shape, T, layers, steps, warmup, name="", tier=None):
     run = em.Runner(dev, shape, T, tier=tier)
     run.gen_inputs(1)
     dev.sync()
-    for _ in range(warmup):
+
+    def step():
         for L in Ls:
             run.forward(L)
+
+    for _ in range(max(1, warmup)):  # eager first: the f16 tier makes its side stream on first use
+        step()
     dev.sync()
     t0 = time.perf_counter()
     for _ in range(steps):
-        for L in Ls:
-            run.forward(L)
+        step()
     dev.sync()
-    wall = time.perf_counter() - t0
+    wall_eager = time.perf_counter() - t0
+    wall = wall_eager
+    launch = "eager"
+    if graph:  # the same launches replayed as one graph a step (as the decode line runs)
+        try:
+            gs = dev.capture(step)
+            dev.replay(gs)
+            dev.sync()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                dev.replay(gs)
+            dev.sync()
+            wall = time.perf_counter() - t0
+            dev.check(dev.lib.llb_hip_graph_free(gs))
+            launch = "one HIP graph a step"
+        except em.LlbError as e:  # keep the eager figure, and say why
+            launch = f"eager (graph capture failed: {e})"
     dev.timing(1)
     dev.check(dev.lib.llb_hip_spin(20000))
     for L in Ls:
@@ -171,9 +190,13 @@ def prefill(dev, shape, T, layers, steps, warmup, name="", tier=None):
         L.free()
     us_layer = wall / (steps * layers) * 1e6
     peak = MFMA_F16_PEAK_TFS if tier == em.F16 else MFMA_I8_PEAK_TOPS
-    kern = "gate_up GEMM (f16 MFMA)" if tier == em.F16 else "gate_up (int8 v_dot4 on q8_1 activations)"
+    q8_mfma = os.environ.get("LLB_MOE_Q8_GEMM", "") == "1"
+    kern = ("gate_up GEMM (f16 MFMA)" if tier == em.F16 else
+            "gate_up GEMM (int8 MFMA on q8_1 activations)" if q8_mfma else "gate_up (int8 v_dot4 on q8_1 activations)")
     return {"tokens_per_s": round(T / (us_layer * 1e-6), 1), "us_per_layer_chunk": round(us_layer, 2), "T": T,
-            "layers": layers, "stages_us": {k: round(v[0], 2) for k, v in st.items()},
+            "layers": layers, "launch": launch,
+            "eager_us_per_layer_chunk": round(wall_eager / (steps * layers) * 1e6, 2),
+            "stages_us": {k: round(v[0], 2) for k, v in st.items()},
             "roofline": {"bound": "mfma", "kernel": kern, "achieved": round(ach, 1),
                          "peak": peak, "unit": "TFLOP/s" if tier == em.F16 else "TOP/s", "frac": round(ach / peak, 4),
                          "traffic": measured_traffic(f"{name}_prefill_{T}", "gate_up", tier == em.F16),
@@ -581,17 +604,19 @@ def main():
     layers.clear()
     if "prefill" in legs:
         pshape = em.SHAPES[args.prefill_config]
-        out["prefill"] = prefill(dev, pshape, args.prefill_T, 4, max(2, args.steps // 4), 1, args.prefill_config)
+        out["prefill"] = prefill(dev, pshape, args.prefill_T, 4, max(2, args.steps // 4), 1, args.prefill_config,
+                                 graph=args.graph)
         out["prefill"]["config"] = f"{args.prefill_config} layer, {args.prefill_T}-token chunk, f16 MFMA tier, packed stacks"
     if "prefill_q8" in legs:
         # the q8 tier (the reference's LLB_PREFILL=fast numerics: q8_1 activations, integer block dots)
         out["prefill_q8"] = prefill(dev, em.SHAPES[args.prefill_config], args.prefill_T, 2, max(2, args.steps // 8), 1,
-                                    args.prefill_config, tier=em.Q8)
+                                    args.prefill_config, tier=em.Q8, graph=args.graph)
         out["prefill_q8"]["config"] = (f"{args.prefill_config} layer, {args.prefill_T}-token chunk, q8 tier "
                                        f"(q8_1 activations, v_dot4 block dots), GGUF stacks")
     if "prefill_k" in legs:
         # the same layer shape with Q4_K gate / up and Q6_K down weight tiles
-        out["prefill_k_quants"] = prefill(dev, em.SHAPES["c1k"], args.prefill_T, 4, max(2, args.steps // 4), 1, "c1k")
+        out["prefill_k_quants"] = prefill(dev, em.SHAPES["c1k"], args.prefill_T, 4, max(2, args.steps // 4), 1, "c1k",
+                                          graph=args.graph)
         out["prefill_k_quants"]["config"] = f"c1k layer (Q4_K gate/up, Q6_K down), {args.prefill_T}-token chunk, f16 MFMA tier, packed stacks"
     if "c5" in legs:
         # config 5: one decode token and a 512-token chunk in one launch, Zipf(1.1) routing, 48 resident
