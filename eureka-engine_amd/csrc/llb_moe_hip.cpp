@@ -195,15 +195,44 @@ int llb_hip_module_function(uint64_t module, const char* name, void** fn) {
   return 0;
 }
 int llb_hip_launch(void* fn, uint32_t gx, uint32_t gy, uint32_t bx, uint32_t sm, void** args, uint32_t na) {
+  return llb_hip_launch3(fn, gx, gy, 1, bx, sm, args, na);
+}
+// the same with a z grid (the fast prefill's grouped launches, host/llb_pf.h:284-285)
+int llb_hip_launch3(void* fn, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx, uint32_t sm, void** args,
+                    uint32_t na) {
   if (!fn) return fail(LLB_HIP_EINVAL, "launch: null kernel");
-  if (!gx || !gy || !bx || bx > 1024) return fail(LLB_HIP_EINVAL, "launch: grid %u x %u of %u threads", gx, gy, bx);
+  if (!gx || !gy || !gz || !bx || bx > 1024)
+    return fail(LLB_HIP_EINVAL, "launch: grid %u x %u x %u of %u threads", gx, gy, gz, bx);
   if (sm > 160 * 1024) return fail(LLB_HIP_EINVAL, "launch: %u bytes of LDS (at most 160 KiB)", sm);
   if (na && !args) return fail(LLB_HIP_EINVAL, "launch: %u arguments but no argument array", na);
   for (uint32_t i = 0; i < na; i++)
     if (!args[i]) return fail(LLB_HIP_EINVAL, "launch: argument %u is a null address", i);
-  return hip_ok(hipModuleLaunchKernel((hipFunction_t)fn, gx, gy, 1, bx, 1, 1, sm, g_stream, na ? args : nullptr,
+  return hip_ok(hipModuleLaunchKernel((hipFunction_t)fn, gx, gy, gz, bx, 1, 1, sm, g_stream, na ? args : nullptr,
                                       nullptr),
                 "hipModuleLaunchKernel");
+}
+// host memory the device reads and writes in place (cuMemHostAlloc(DEVICEMAP | PORTABLE) +
+// cuMemHostGetDevicePointer, host/llb_host.c:446-489): pinned, mapped, and its device address
+int llb_hip_host_alloc(size_t bytes, void** host, llb_dptr* dev) {
+  if (!host || !dev) return fail(LLB_HIP_EINVAL, "host_alloc: null argument");
+  void* h = nullptr;
+  int rc = hip_ok(hipHostMalloc(&h, bytes ? bytes : 4, hipHostMallocMapped | hipHostMallocPortable), "hipHostMalloc");
+  if (rc) return rc;
+  void* d = nullptr;
+  if ((rc = hip_ok(hipHostGetDevicePointer(&d, h, 0), "hipHostGetDevicePointer"))) {
+    (void)hipHostFree(h);
+    return rc;
+  }
+  *host = h;
+  *dev = (llb_dptr)(uintptr_t)d;
+  return 0;
+}
+int llb_hip_host_free(void* host) { return host ? hip_ok(hipHostFree(host), "hipHostFree") : 0; }
+// host bytes into device memory in stream order, no wait (cuMemcpyHtoDAsync, host/llb_host.c:691-693): the
+// host buffer must stay as it is until the copy has run (pinned memory for a copy that overlaps)
+int llb_hip_copy_h2d_async(llb_dptr d, const void* h, size_t bytes) {
+  if (bytes && (!d || !h)) return fail(LLB_HIP_EINVAL, "copy_h2d_async: null buffer");
+  return hip_ok(hipMemcpyAsync(dp<void>(d), h, bytes, hipMemcpyHostToDevice, g_stream), "copy_h2d_async");
 }
 
 // graph record / replay (llb_graph_begin / llb_graph_end, host/llb_backend_cuda.h:125-184): the

@@ -60,6 +60,11 @@ _SIGS = {
     "llb_hip_module_function": (C.c_int, [C.c_uint64, C.c_char_p, C.POINTER(C.c_void_p)]),
     "llb_hip_launch": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                  C.POINTER(C.c_void_p), C.c_uint32]),
+    "llb_hip_launch3": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                  C.POINTER(C.c_void_p), C.c_uint32]),
+    "llb_hip_host_alloc": (C.c_int, [C.c_size_t, C.POINTER(C.c_void_p), C.POINTER(C.c_uint64)]),
+    "llb_hip_host_free": (C.c_int, [C.c_void_p]),
+    "llb_hip_copy_h2d_async": (C.c_int, [C.c_uint64, C.c_void_p, C.c_size_t]),
     "llb_hip_graph_begin": (C.c_int, []),
     "llb_hip_graph_end": (C.c_int, [C.POINTER(C.c_uint64)]),
     "llb_hip_graph_launch": (C.c_int, [C.c_uint64]),

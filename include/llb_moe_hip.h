@@ -62,6 +62,15 @@ int llb_hip_mem_info(size_t* free_bytes, size_t* total_bytes); /* cuMemGetInfo, 
 int llb_hip_module_load(const char* path, uint64_t* module);
 int llb_hip_module_function(uint64_t module, const char* name, void** fn);
 int llb_hip_launch(void* fn, uint32_t gx, uint32_t gy, uint32_t bx, uint32_t sm, void** args, uint32_t na);
+/* with a z grid (the fast prefill's direct cuLaunchKernel, host/llb_pf.h:284-285) */
+int llb_hip_launch3(void* fn, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx, uint32_t sm, void** args,
+                    uint32_t na);
+/* pinned, device-mapped host memory and its device address (cuMemHostAlloc(DEVICEMAP | PORTABLE) +
+ * cuMemHostGetDevicePointer, host/llb_host.c:446-489), and its release */
+int llb_hip_host_alloc(size_t bytes, void** host, llb_dptr* dev);
+int llb_hip_host_free(void* host);
+/* host to device in stream order without waiting (cuMemcpyHtoDAsync, host/llb_host.c:691-693) */
+int llb_hip_copy_h2d_async(llb_dptr d, const void* h, size_t bytes);
 /* graph record / replay: llb_graph_begin / llb_graph_end (host/llb_backend_cuda.h:125-184). Launches
  * between begin and end are captured (not run); launch replays them on the library's stream.
  * No allocation, copy or read may happen inside a capture (the reference bails to eager there). */
