@@ -10,8 +10,6 @@
 // then y[t] = (sum over ranks j, in order, wt[t][j] out[inv[t nk + j]]) + sgo[t] shd[t] + x1[t].
 // The shared expert is the same two GEMMs over all T tokens (one "expert", identity map).
 //
-#include <stdlib.h>
-
 #include "../../include/llb_moe_hip.h"
 #include "moe_dev.h"
 #include "moe_kernels.h"
@@ -371,159 +369,6 @@ DEV void gemm3_body(const GemmArgs& g, _Float16* lds, u32 e, u32 base, u32 m0, u
     }
 }
 
-// ---- the same tile, software-pipelined inside the wave: step t multiplies tile t with weights
-// decoded during step t - 1 while it decodes tile t + 1's weights, and the schedule interleaves the two
-// (one MFMA, then a share of the decode's VALU), so a single wave keeps the matrix core busy through the
-// decode instead of alternating the two. The decoded B operands of two k-tiles stay in registers (D0,
-// D1, 32 dwords each), and a slot's raw loads are refilled as soon as they are decoded (tile t + 3 at
-// the start of step t). Same loads, LDS stages, barriers and products as gemm3_body, so the same bits.
-template <u32 F, u32 MODE, bool PKD, u32 NL>
-DEV void gemm3p_body(const GemmArgs& g, _Float16* lds, u32 e, u32 base, u32 m0, u32 M, u32 ntile) {
-  const u32 tid = threadIdx.x, w = tid >> 6, l = tid & 63, h = l >> 5, lr = l & 31;
-  const __amdgpu_buffer_rsrc_t arsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)g.A, (short)0, (int)(g.arows * g.K * 2u), 0x00020000);
-  u32 aoff[NL], src[NL];
-#pragma unroll
-  for (u32 i = 0; i < NL; i++) src[i] = base + m0 + min(32 * i + (tid >> 3), M - m0 - 1);
-  if (MODE == 0 && g.xmap) {
-#pragma unroll
-    for (u32 i = 0; i < NL; i++) src[i] = g.xmap[src[i]];
-  }
-#pragma unroll
-  for (u32 i = 0; i < NL; i++)
-    aoff[i] = m0 + 32 * i + (tid >> 3) < M ? (src[i] * g.K + 8 * (tid & 7)) * 2u : 0x80000000u;
-  const u32 nk = g.K / G3_BK;
-  const u8 *br0, *br1;
-  if constexpr (PKD) {
-    const u64 g0 = MODE == 0 ? 4 * ntile + w : 8 * ntile + 2 * w, tb = (u64)nk * PK<F>::TB;
-    br0 = g.P0 + (u64)e * g.pes + g0 * tb;
-    br1 = MODE == 0 ? g.P1 + (u64)e * g.pes + g0 * tb : br0 + tb;
-  } else if (MODE == 0) {
-    const u64 f = (u64)ntile * 128 + 32 * w + lr;
-    br0 = g.W0 + (u64)e * g.es + f * g.rb;
-    br1 = g.W1 + (u64)e * g.es + f * g.rb;
-  } else {
-    const u64 n = (u64)ntile * 256 + 64 * w + lr;
-    br0 = g.W0 + (u64)e * g.es + n * g.rb;
-    br1 = br0 + 32 * g.rb;
-  }
-  struct Slot {
-    uint4 a[NL];
-    BRow<F, PKD> b0, b1;
-  };
-  // decoded B of one k-tile: [0] row b0 half 0, [1] b0 half 1, [2] b1 half 0, [3] b1 half 1
-  struct Dec {
-    u32 o[4][8];
-  };
-  Slot s0, s1, s2;
-  Dec d0, d1;
-  auto load = [&](Slot& s, u32 t) {
-    const u32 tc = min(t, nk - 1), k0 = tc * G3_BK;
-#pragma unroll
-    for (u32 i = 0; i < NL; i++) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(arsrc, (int)(aoff[i] + 2 * k0), 0, 0);
-      s.a[i] = make_uint4(v[0], v[1], v[2], v[3]);
-    }
-    s.b0.ld(br0, tc, l);
-    s.b1.ld(br1, tc, l);
-  };
-  auto store = [&](const Slot& s, u32 t) {
-    _Float16* As = lds + (t & 1) * G3_STAGE;
-#pragma unroll
-    for (u32 i = 0; i < NL; i++) *(uint4*)(As + (32 * i + (tid >> 3)) * G3_LD + 8 * (tid & 7)) = s.a[i];
-  };
-  auto decode = [&](const Slot& s, u32 q, u32* o) {
-    if (q == 0) s.b0.f16(0, o);
-    else if (q == 1) s.b0.f16(1, o);
-    else if (q == 2) s.b1.f16(0, o);
-    else s.b1.f16(1, o);
-  };
-  f32x16 acc[NL][2];
-#pragma unroll
-  for (u32 a = 0; a < NL; a++)
-#pragma unroll
-    for (u32 b = 0; b < 2; b++)
-#pragma unroll
-      for (u32 i = 0; i < 16; i++) acc[a][b][i] = 0.0f;
-  // step t: X holds tile t's raw loads (already decoded into D), Y tile t + 1's (decoded here into N)
-  auto step = [&](Slot& X, const Slot& Y, const Dec& D, Dec& N, u32 t) {
-    // at the last tile Y repeats it (loads clamp to tile nk - 1): storing and decoding it anyway keeps
-    // the step one basic block for the scheduler; nothing reads that stage or N afterwards
-    load(X, t + 3);
-    store(Y, t + 1);
-    const _Float16* As = lds + (t & 1) * G3_STAGE + lr * G3_LD + 32 * h;
-#pragma unroll
-    for (u32 st = 0; st < 4; st++) {
-      decode(Y, st, N.o[st]);
-      const u32* p0 = D.o[st < 2 ? 0 : 1];
-      const u32* p1 = D.o[st < 2 ? 2 : 3];
-      const u32 j = 4 * (st & 1);
-      h8 b0, b1;
-      __builtin_memcpy(&b0, p0 + j, 16);
-      __builtin_memcpy(&b1, p1 + j, 16);
-#pragma unroll
-      for (u32 mf = 0; mf < NL; mf++) {
-        const h8 a = *(const h8*)(As + 32 * mf * G3_LD + 8 * st);
-        acc[mf][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b0, acc[mf][0], 0, 0, 0);
-        acc[mf][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b1, acc[mf][1], 0, 0, 0);
-      }
-    }
-    // one MFMA, then a share of the decode, through the step
-#pragma unroll
-    for (u32 i = 0; i < 4 * 2 * NL; i++) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, NL == 1 ? 14 : 7, 0);
-    }
-    __syncthreads();
-  };
-  load(s0, 0);
-  load(s1, 1);
-  load(s2, 2);
-  store(s0, 0);
-#pragma unroll
-  for (u32 q = 0; q < 4; q++) decode(s0, q, d0.o[q]);
-  __syncthreads();
-  // tiles rotate through three slots and two decoded buffers: six steps a round
-  u32 t = 0;
-  for (; t + 6 <= nk; t += 6) {
-    step(s0, s1, d0, d1, t);
-    step(s1, s2, d1, d0, t + 1);
-    step(s2, s0, d0, d1, t + 2);
-    step(s0, s1, d1, d0, t + 3);
-    step(s1, s2, d0, d1, t + 4);
-    step(s2, s0, d1, d0, t + 5);
-  }
-  if (t < nk) step(s0, s1, d0, d1, t);
-  if (t + 1 < nk) step(s1, s2, d1, d0, t + 1);
-  if (t + 2 < nk) step(s2, s0, d0, d1, t + 2);
-  if (t + 3 < nk) step(s0, s1, d1, d0, t + 3);
-  if (t + 4 < nk) step(s1, s2, d0, d1, t + 4);
-#pragma unroll
-  for (u32 mf = 0; mf < NL; mf++)
-#pragma unroll
-    for (u32 i = 0; i < 16; i++) {
-      const u32 row = 32 * mf + 8 * (i >> 2) + 4 * h + (i & 3);
-      if (m0 + row >= M) continue;
-      const u64 s = base + m0 + row;
-      if (MODE == 0) {
-        const float gv = acc[mf][0][i], uv = acc[mf][1][i];
-        ((_Float16*)g.out)[s * g.N + ntile * 128 + 32 * w + lr] = (_Float16)(gv / (1.0f + __expf(-gv)) * uv);
-      } else {
-#pragma unroll
-        for (u32 b = 0; b < 2; b++) {
-          const u64 o = s * g.N + ntile * 256 + 64 * w + 32 * b + lr;
-          if (g.o16) {
-            const _Float16 hv = (_Float16)acc[mf][b][i];
-            ((_Float16*)g.out)[o] = hv;
-            if (__builtin_isinf((float)hv)) g.spill[o] = acc[mf][b][i];
-          } else {
-            ((float*)g.out)[o] = acc[mf][b][i];
-          }
-        }
-      }
-    }
-}
-
 // XCD-aware order: the hardware deals block b to XCD b % 8. XCD x takes the contiguous chunk of the
 // tile list [x C, x C + C), C = ceil(tiles / 8), and walks it tile by tile, each tile's NT weight-row
 // tiles in a row (block b: tile x C + (b / 8) / NT, weight-row tile (b / 8) % NT). So a tile's blocks
@@ -531,8 +376,7 @@ DEV void gemm3p_body(const GemmArgs& g, _Float16* lds, u32 e, u32 base, u32 m0, 
 // run on one XCD at about the same time and share its weight slices there (1-D grid,
 // 8 NT ceil(max tiles / 8) blocks). Blocks a CU: three on packed weights, two on GGUF rows (whose
 // wider per-lane loads need more registers) and for packed Q8_0 gate / up (which would spill at three).
-// The pipelined body holds two k-tiles' decoded weights, so it runs two blocks a CU.
-constexpr int g3_blocks(u32 F, u32 MODE, bool PKD, bool PIPE) { return !PIPE && PKD && !(F == FM_Q8_0 && MODE == 0) ? 3 : 2; }
+constexpr int g3_blocks(u32 F, u32 MODE, bool PKD) { return PKD && !(F == FM_Q8_0 && MODE == 0) ? 3 : 2; }
 // The tile list, read off the slot offsets: expert e has ceil(M_e / BM) slot tiles, listed in expert
 // order. Every wave loads the ne + 1 offsets once (16 chunks of 64 experts at most, all loads in
 // flight together), sums the tile counts, and finds tile `tile` by an inclusive scan of the counts
@@ -581,8 +425,8 @@ DEV void tiles_find(const u32* te, u32 ne, u32 tile, u32 L, u32& e, u32& k) {
   }
 }
 
-template <u32 F, u32 MODE, bool PKD, bool PIPE>
-__global__ void __launch_bounds__(256, g3_blocks(F, MODE, PKD, PIPE)) k_moe_gemm3(GemmArgs g, u32 NT) {
+template <u32 F, u32 MODE, bool PKD>
+__global__ void __launch_bounds__(256, g3_blocks(F, MODE, PKD)) k_moe_gemm3(GemmArgs g, u32 NT) {
   extern __shared__ _Float16 lds[];
   const u32 q = blockIdx.x >> 3, ntile = q % NT, L = threadIdx.x & 63;
   u32 te[G3_NEC];
@@ -611,13 +455,8 @@ __global__ void __launch_bounds__(256, g3_blocks(F, MODE, PKD, PIPE)) k_moe_gemm
     M = g.M;
   }
   static_assert(G3_MF == 2, "one or two live fragments");
-  if constexpr (PIPE) {
-    if (M - m0 <= 32) gemm3p_body<F, MODE, PKD, 1>(g, lds, e, base, m0, M, ntile);
-    else gemm3p_body<F, MODE, PKD, 2>(g, lds, e, base, m0, M, ntile);
-  } else {
-    if (M - m0 <= 32) gemm3_body<F, MODE, PKD, 1>(g, lds, e, base, m0, M, ntile);
-    else gemm3_body<F, MODE, PKD, 2>(g, lds, e, base, m0, M, ntile);
-  }
+  if (M - m0 <= 32) gemm3_body<F, MODE, PKD, 1>(g, lds, e, base, m0, M, ntile);
+  else gemm3_body<F, MODE, PKD, 2>(g, lds, e, base, m0, M, ntile);
 }
 
 // y[t][r] = (sum_j, rank order, wt[t][j] out[inv[t nk + j]][r]) + sgo[t] shd[t][r] + x1[t][r]; the slots'
@@ -938,24 +777,13 @@ int launch_gemm_i8(const GemmQ8Args& g, u32 fm, u32 mode, u32 grid_y, hipStream_
 
 // ---------------------------------------------------------------- launchers
 
-// LLB_MOE_GEMM_PIPE=1 selects the in-wave pipelined body for packed weights (read at each launch)
-static bool gemm_pipe_on() {
-  const char* v = getenv("LLB_MOE_GEMM_PIPE");
-  return v && v[0] == '1';
-}
-template <u32 F, u32 MODE, bool PKD, bool PIPE> static void gemm3_go1(const GemmArgs& g, dim3 grid, size_t sm, hipStream_t st) {
+template <u32 F, u32 MODE, bool PKD> static void gemm3_go(const GemmArgs& g, dim3 grid, size_t sm, hipStream_t st) {
   static bool set = false;
   if (!set) {
-    (void)hipFuncSetAttribute((const void*)k_moe_gemm3<F, MODE, PKD, PIPE>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
+    (void)hipFuncSetAttribute((const void*)k_moe_gemm3<F, MODE, PKD>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
     set = true;
   }
-  LAUNCH_K((k_moe_gemm3<F, MODE, PKD, PIPE>), grid, dim3(256), sm, st, g, g.N / (MODE == 0 ? 128u : 256u));
-}
-template <u32 F, u32 MODE, bool PKD> static void gemm3_go(const GemmArgs& g, dim3 grid, size_t sm, hipStream_t st) {
-  if constexpr (PKD) {
-    if (gemm_pipe_on()) return gemm3_go1<F, MODE, true, true>(g, grid, sm, st);
-  }
-  gemm3_go1<F, MODE, PKD, false>(g, grid, sm, st);
+  LAUNCH_K((k_moe_gemm3<F, MODE, PKD>), grid, dim3(256), sm, st, g, g.N / (MODE == 0 ? 128u : 256u));
 }
 
 int launch_moe_gemm(const GemmArgs& g, u32 fm, u32 mode, u32 grid_y, hipStream_t st) {
