@@ -287,14 +287,22 @@ int llb_moe_table_from_gguf(const llb_gguf* g, uint32_t* table, uint32_t cap, ui
   if (g->arch != "qwen35moe") return llb_fail_msg(LLB_HIP_EINVAL, "table: general.architecture is not qwen35moe");
   int64_t L0 = 0, ne = 0, nk = 0, ef = 0, sf = 0, mtp = 0;
   const std::string a = g->arch + ".";
-  if (!gg_int(g, a + "block_count", &L0) || !gg_int(g, a + "expert_count", &ne) ||
+  int64_t D = 0;
+  if (!gg_int(g, a + "block_count", &L0) || !gg_int(g, a + "embedding_length", &D) || !gg_int(g, a + "expert_count", &ne) ||
       !gg_int(g, a + "expert_used_count", &nk) || !gg_int(g, a + "expert_feed_forward_length", &ef) ||
       !gg_int(g, a + "expert_shared_feed_forward_length", &sf))
     return llb_fail_msg(LLB_HIP_EINVAL, "table: a qwen35moe expert / block count key is missing");
   gg_int(g, a + "nextn_predict_layers", &mtp);
-  if (L0 < 1 || L0 > 4096 || ne < 1 || ne > 0xffffffffll || nk < 1 || nk > ne || ef < 1 || sf < 1 || mtp < 0 ||
+  if (L0 < 1 || L0 > 4096 || D < 1 || ne < 1 || ne > 0xffffffffll || nk < 1 || nk > ne || ef < 1 || sf < 1 || mtp < 0 ||
       mtp >= L0)
     return llb_fail_msg(LLB_HIP_EINVAL, "table: implausible block / expert counts");
+  {  // a name twice is refused (tools/gguf2pack.c:1187-1189)
+    std::vector<const std::string*> nm;
+    for (const auto& t : g->t) nm.push_back(&t.name);
+    std::sort(nm.begin(), nm.end(), [](const std::string* x, const std::string* y) { return *x < *y; });
+    for (size_t i = 1; i < nm.size(); i++)
+      if (*nm[i] == *nm[i - 1]) return llb_fail_msg(LLB_HIP_EINVAL, ("table: " + *nm[i] + ": duplicate tensor").c_str());
+  }
   const uint32_t nl = (uint32_t)(L0 - mtp);
   *nlayers = nl;
   if (!table || cap < nl) return llb_fail_msg(LLB_HIP_EINVAL, "table: the table holds fewer rows than layers");
@@ -352,6 +360,13 @@ int llb_moe_table_from_gguf(const llb_gguf* g, uint32_t* table, uint32_t cap, ui
       w[1 + j] = (uint32_t)rel | fm << 28;
       if (router) need[L * 6 + 0] = 1;
       if (shgate) need[L * 6 + 1] = 1;
+      // the router is F32 [expert_count x d_model], the shared gate row F32 [d_model] (or [1 x d_model])
+      // (tools/gguf2pack.c:1253-1257); GGUF dims run columns first
+      const GgTensor& t = g->t[i];
+      if (router && (t.type != 0 || t.nd != 2 || t.dims[0] != (uint64_t)D || t.dims[1] != (uint64_t)ne))
+        return llb_fail_msg(LLB_HIP_EINVAL, ("table: " + nm + ": the router must be F32 [expert_count x d_model]").c_str());
+      if (shgate && (t.type != 0 || t.dims[0] != (uint64_t)D || !(t.nd == 1 || (t.nd == 2 && t.dims[1] == 1))))
+        return llb_fail_msg(LLB_HIP_EINVAL, ("table: " + nm + ": the shared-expert gate must be F32 [d_model]").c_str());
       continue;
     }
     const int x = s == "ffn_gate_exps.weight" || s == "ffn_gate_up_exps.weight" ? 0
@@ -361,6 +376,15 @@ int llb_moe_table_from_gguf(const llb_gguf* g, uint32_t* table, uint32_t cap, ui
     if (x < 0) return llb_fail_msg(LLB_HIP_EINVAL, ("table: " + nm + ": a tensor outside the MoE table").c_str());
     const bool fz = s == "ffn_gate_up_exps.weight";
     need[L * 6 + (fz ? 4 : x == 0 ? 2 : x == 1 ? 3 : 5)] = 1;
+    {  // [expert_count x rows x cols] in Q8_0 / Q4_K / Q5_K / Q6_K (tools/gguf2pack.c:1258-1268)
+      const GgTensor& t = g->t[i];
+      const uint64_t rows = x == 2 ? (uint64_t)D : fz ? 2 * (uint64_t)ef : (uint64_t)ef;
+      const uint64_t cols = x == 2 ? (uint64_t)ef : (uint64_t)D;
+      if (t.nd != 3 || t.dims[2] != (uint64_t)ne || t.dims[1] != rows || t.dims[0] != cols)
+        return llb_fail_msg(LLB_HIP_EINVAL, ("table: " + nm + ": an expert stack of the wrong shape").c_str());
+      if (t.type != 8 && t.type != 12 && t.type != 13 && t.type != 14)
+        return llb_fail_msg(LLB_HIP_EINVAL, ("table: " + nm + ": expert stacks take Q8_0, Q4_K, Q5_K, Q6_K").c_str());
+    }
     w[26] |= fm << (4 * x) | (fz ? 1u << 12 : 0u) | 1u << 13;
   }
   for (uint32_t L = 0; L < nl; L++) {

@@ -133,3 +133,45 @@ def test_refuses_a_layer_without_its_stacks(tmp_path):
         assert b"stacks" in lib.llb_hip_last_error()
     finally:
         lib.llb_gguf_close(g)
+
+
+def _edit(ts, name, ty=None, dims=None):
+    out = []
+    for t in ts:
+        if t[0] == name:
+            t = _t(name, t[1] if ty is None else ty, t[2] if dims is None else dims)
+        out.append(t)
+    return out
+
+
+D_, NE_, EF_ = D, CASES["kquants"]["ne"], CASES["kquants"]["ef"]
+BAD = {
+    "duplicate": lambda ts: ts + [_t("blk.0.ssm_a", 0, (TR,))],
+    "router_q8": lambda ts: _edit(ts, "blk.0.ffn_gate_inp.weight", ty=8),
+    "router_shape": lambda ts: _edit(ts, "blk.1.ffn_gate_inp.weight", dims=(D_, NE_ + 1)),
+    "shgate_shape": lambda ts: _edit(ts, "blk.0.ffn_gate_inp_shexp.weight", dims=(D_, 2)),
+    "gate_experts": lambda ts: _edit(ts, "blk.0.ffn_gate_exps.weight", dims=(D_, EF_, NE_ - 1)),
+    "down_rows": lambda ts: _edit(ts, "blk.1.ffn_down_exps.weight", dims=(EF_, 2 * D_, NE_)),
+    "up_f32": lambda ts: _edit(ts, "blk.1.ffn_up_exps.weight", ty=0),
+}
+
+
+@pytest.mark.parametrize("bad", sorted(BAD))
+def test_refuses_what_the_reference_sidecar_refuses(tmp_path, bad):
+    """the reference's sidecar writer dies on these files (duplicate names, a router or shared gate that is
+    not F32 of its shape, expert stacks of the wrong shape or format); the table builder refuses them too"""
+    ts, kv = model(**CASES["kquants"])
+    path = str(tmp_path / "m.gguf")
+    gguf_io.write(path, BAD[bad](ts), alignment=32, extra_kv=kv)
+    g = lib.llb_gguf_open(path.encode())
+    assert g, lib.llb_hip_last_error()
+    try:
+        tab, nl = (C.c_uint32 * 256)(), C.c_uint32()
+        assert lib.llb_moe_table_from_gguf(g, tab, 8, C.byref(nl)) != 0
+        assert lib.llb_hip_last_error().startswith(b"table: ")
+    finally:
+        lib.llb_gguf_close(g)
+    if os.path.exists(G2P):
+        r = subprocess.run([G2P, path, "--sidecar-only", str(tmp_path / "side")], capture_output=True, text=True,
+                           timeout=120)
+        assert r.returncode != 0, r.stdout
