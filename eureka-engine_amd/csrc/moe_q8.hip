@@ -243,8 +243,11 @@ static bool q8_gemm_on() {
 }
 static bool q8_gemm_ok(const llb_moe_layer* L, uint32_t T) {
   const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15;
+  const uint32_t fd = L->fx >> 8 & 15;
+  // launch_gemm_i8 takes K-quant rows of whole 256-column super-blocks only (down: K = ef; shared down: sf)
+  const bool kd = fd == FM_Q8_0 || L->ef % 256 == 0, ks = !L->sf || L->fsd == FM_Q8_0 || L->sf % 256 == 0;
   return q8_gemm_on() && T >= Q8_GEMM_T && fg == fu && (!L->sf || L->fsg == L->fsu) && L->ef % 128 == 0 && L->sf % 128 == 0 &&
-         L->dm % 256 == 0 && L->ne <= 1024;
+         L->dm % 256 == 0 && L->ne <= 1024 && kd && ks;
 }
 size_t moe_q8_scratch(const llb_moe_layer* L, uint32_t T) {
   const size_t n = (size_t)T * L->nk;
