@@ -27,8 +27,7 @@
 #include "moe_kernels.h"
 #include "moe_q8dot.h"
 
-// per-block wall-clock stamps for latency studies (100 MHz): a build that defines MOE_PHASE_T records
-// stamp i of block b of thread 0 (and of thread 64, stamps >= 8 of k_gu_dec) in dec_stamp[i][b]; the
+// per-block clock stamps for latency studies: a build that defines MOE_DEC_STAMPS records them; the
 // library build compiles them away
 #ifdef MOE_DEC_STAMPS
 // stamp i of block b (thread 0; stamps 8..15 of k_gu_dec from thread 960, its last wave) in shader clocks
@@ -758,9 +757,9 @@ __global__ void __launch_bounds__(1024) k_gu_dec(DecGuArgs a) {
   DSTAMP(7);
   DSTAMP(10);
   // the down launch's rows for its block b3 = blockIdx (same XCD, so the same L2): task w's DN_RB rows,
-  // one dword a 128-byte line, issued once this wave's own rows have landed. The load is an asm
-  // statement, so the compiler neither moves it nor counts it in its waits; the data is never used,
-  // only waited for at the end.
+  // one dword a 128-byte line, issued once this wave's own rows have landed. It is a plain load held in
+  // place by a scheduling barrier; its value feeds only an empty asm statement at the end, so the wait
+  // for it comes last.
   u32 touch = 0;
   {
     // waves past the tasks, and grids where this block has no down block, touch expert 0's first line
@@ -771,9 +770,12 @@ __global__ void __launch_bounds__(1024) k_gu_dec(DecGuArgs a) {
                         : a.D + ((u64)ids_s[min(w, a.nk - 1)] * a.dm + DN_RB_G * b3) * rb;
     // (pointer arithmetic, not integers, so the load stays a global load: a flat one would also count
     // against the LDS wait counter)
+    // line L of the rows: its first dword, but never below base (line 0 when base is not 128-aligned,
+    // which for expert 0 would read before the stack) and never past the rows' last byte
     const u8* lo = base - ((u32)(uintptr_t)base & 127u);
-    const bool live = w < a.nk + (a.SD ? 1u : 0u) && lo + 128 * L < base + DN_RB_G * rb;
-    touch = *(const u32*)(live ? lo + 128 * L : a.D);
+    const u8* p = L == 0 ? base : lo + 128 * L;
+    const bool live = w < a.nk + (a.SD ? 1u : 0u) && p + 4 <= base + DN_RB_G * rb;
+    touch = *(const u32*)(live ? p : a.D);
     __builtin_amdgcn_sched_barrier(0);
   }
   float sv;

@@ -352,6 +352,24 @@ float mo_gemv_row(u32 fm, const u8* row, u32 cols, const float* x) {
 float mo_exp(float x) { return (float)exp((double)x); }
 /* llb_moe_gu's epilogue (tools/payload-moeany.patch:495): silu(g) * u = (g / (1 + exp(-g))) * u */
 float mo_silu_mul(float g, float u) { return (g / (1.0f + mo_exp(-g))) * u; }
+/* llb_moe_topk's shared gate (tools/payload-moeany.patch:468): 1 / (1 + exp(-sg)) */
+float mo_sigmoid(float x) { return 1.0f / (1.0f + mo_exp(-x)); }
+/* llb_moe_topk's renormalisation (tools/payload-moeany.patch:459-467): s = the k weights summed in rank
+ * order from 0.0f, clamped below at 2^-14; each weight divided by s */
+void mo_renorm(float* wt, u32 nk) {
+  float s = 0.0f;
+  for (u32 j = 0; j < nk; j++) s = s + wt[j];
+  s = s < 6.103515625e-5f ? 6.103515625e-5f : s;
+  for (u32 j = 0; j < nk; j++) wt[j] = wt[j] / s;
+}
+/* llb_moe_dn's combine for one output row (tools/payload-moeany.patch:572-592): mo = v0 wt0 (the first
+ * term itself, not 0 + v0 wt0), then mo + vj wtj in rank order, each product rounded before its add;
+ * y = (mo + hv sgo) + res with the shared expert, mo + res without */
+float mo_combine(const float* v, const float* wt, u32 nk, int shared, float hv, float sgo, float res) {
+  float mo = 0.0f;
+  for (u32 j = 0; j < nk; j++) mo = j == 0 ? v[0] * wt[0] : mo + v[j] * wt[j];
+  return shared ? (mo + hv * sgo) + res : mo + res;
+}
 
 /* ------------------------------------------------------------------ routing */
 
@@ -401,11 +419,8 @@ void mo_topk(const float* lg, u32 ne, u32 nk, float sg, u32* ids, float* wt, flo
     wt[j] = bv;
     p[bi] = -2.0f;
   }
-  float s = 0.0f;
-  for (u32 j = 0; j < nk; j++) s = s + wt[j];
-  s = s < 6.103515625e-5f ? 6.103515625e-5f : s;
-  for (u32 j = 0; j < nk; j++) wt[j] = wt[j] / s;
-  *sgo = 1.0f / (1.0f + mo_exp(-sg));
+  mo_renorm(wt, nk);
+  *sgo = mo_sigmoid(sg);
   free(p);
 }
 
@@ -428,7 +443,7 @@ void mo_group(const u32* ids, u32 n, u32 nk, u32 ne, u32* off, u32* xmap, u32* i
 /* ------------------------------------------------------------------ the layer (exact) */
 
 static int layer_ok(const mo_layer* L) {
-  if (!L->dm || !L->ne || !L->nk || L->nk > L->ne || !L->ef) return 0;
+  if (!L->dm || !L->ne || !L->nk || L->nk > L->ne || L->nk > 64 || !L->ef) return 0;
   if (!mo_row_bytes(L->fg, L->dm) || !mo_row_bytes(L->fu, L->dm) || !mo_row_bytes(L->fd, L->ef)) return 0;
   if (L->fg == MO_F32 || L->fu == MO_F32 || L->fd == MO_F32) return 0;
   if (L->dm % 256 || L->ef % 256) return 0;
@@ -491,20 +506,14 @@ int mo_moe_exact(const mo_layer* L, u32 T, const float* h2, const float* x1, flo
     const float so = sgo[t];
 #pragma omp parallel for num_threads(nt) if (nt > 1) schedule(static)
     for (long long r = 0; r < (long long)dm; r++) {
-      /* llb_moe_dn (tools/payload-moeany.patch:543-594): mo = v0 wt0, then mo + vj wtj in rank
-       * order; y = (mo + hv sgo) + x1, hv the shared down row (llb_kgemv's order for it) */
-      float mo = 0.0f;
-      for (u32 j = 0; j < nk; j++) {
-        float v = mo_dot_stride(L->fd, L->D + ((u64)id[j] * dm + (u64)r) * rbd, ef, act + (size_t)j * ef);
-        mo = j == 0 ? v * w[0] : mo + v * w[j];
-      }
-      float res = x1 ? x1[(size_t)t * dm + r] : 0.0f;
-      if (sf) {
-        float hv = mo_gemv_row(L->fsd, L->SD + (u64)r * rbs, sf, sa);
-        y[(size_t)t * dm + r] = (mo + hv * so) + res;
-      } else {
-        y[(size_t)t * dm + r] = mo + res;
-      }
+      /* llb_moe_dn (tools/payload-moeany.patch:543-594): the routed down dots, hv the shared down row
+       * (llb_kgemv's order for it), then the combine */
+      float v[64];
+      for (u32 j = 0; j < nk; j++)
+        v[j] = mo_dot_stride(L->fd, L->D + ((u64)id[j] * dm + (u64)r) * rbd, ef, act + (size_t)j * ef);
+      const float res = x1 ? x1[(size_t)t * dm + r] : 0.0f;
+      const float hv = sf ? mo_gemv_row(L->fsd, L->SD + (u64)r * rbs, sf, sa) : 0.0f;
+      y[(size_t)t * dm + r] = mo_combine(v, w, nk, sf != 0, hv, so, res);
     }
   }
   free(lg); free(act); free(sa);
@@ -627,19 +636,13 @@ int mo_moe_q8(const mo_layer* L, u32 T, const float* h2, const float* x1, float*
     const float so = sgo[t];
 #pragma omp parallel for num_threads(nt) if (nt > 1) schedule(static)
     for (long long r = 0; r < (long long)dm; r++) {
-      float mo = 0.0f;
-      for (u32 j = 0; j < nk; j++) {
-        float v = mo_dot_q8(L->fd, L->D + ((u64)id[j] * dm + (u64)r) * rbd, ef, aq + (size_t)j * ef,
-                            ad + (size_t)j * ef / 32, as + (size_t)j * ef / 32);
-        mo = j == 0 ? v * w[0] : mo + v * w[j];
-      }
-      float res = x1 ? x1[(size_t)t * dm + r] : 0.0f;
-      if (sf) {
-        float hv = mo_dot_q8(L->fsd, L->SD + (u64)r * rbs, sf, sqb, sd, ss);
-        y[(size_t)t * dm + r] = (mo + hv * so) + res;
-      } else {
-        y[(size_t)t * dm + r] = mo + res;
-      }
+      float v[64];
+      for (u32 j = 0; j < nk; j++)
+        v[j] = mo_dot_q8(L->fd, L->D + ((u64)id[j] * dm + (u64)r) * rbd, ef, aq + (size_t)j * ef,
+                         ad + (size_t)j * ef / 32, as + (size_t)j * ef / 32);
+      const float res = x1 ? x1[(size_t)t * dm + r] : 0.0f;
+      const float hv = sf ? mo_dot_q8(L->fsd, L->SD + (u64)r * rbs, sf, sqb, sd, ss) : 0.0f;
+      y[(size_t)t * dm + r] = mo_combine(v, w, nk, sf != 0, hv, so, res);
     }
     free(sd); free(ss); free(sqb);
   }

@@ -71,6 +71,9 @@ float mo_dot_tree(uint32_t fm, const uint8_t* row, uint32_t cols, const float* x
 float mo_gemv_row(uint32_t fm, const uint8_t* row, uint32_t cols, const float* x);
 float mo_exp(float x);
 float mo_silu_mul(float g, float u);
+float mo_sigmoid(float x);
+void mo_renorm(float* wt, uint32_t nk);
+float mo_combine(const float* v, const float* wt, uint32_t nk, int shared, float hv, float sgo, float res);
 
 /* ---- routing ---- */
 void mo_router(const mo_layer* L, const float* h2, float* lg, float* sg);

@@ -60,6 +60,9 @@ _SIGS = {
     "mo_q8_1": (None, [P, C.c_uint32, P, P, P]),
     "mo_dot_q8": (C.c_float, [C.c_uint32, P, C.c_uint32, P, P, P]),
     "mo_rmsnorm_add": (C.c_float, [P, P, P, C.c_float, C.c_uint32, P, P]),
+    "mo_sigmoid": (C.c_float, [C.c_float]),
+    "mo_renorm": (None, [P, C.c_uint32]),
+    "mo_combine": (C.c_float, [P, P, C.c_uint32, C.c_int, C.c_float, C.c_float, C.c_float]),
 }
 
 _lib = None
