@@ -64,6 +64,10 @@ static bool gg_block(uint32_t ty, uint64_t& bb, uint64_t& be) {
     case 12: bb = 144; be = 256; return true; // Q4_K
     case 13: bb = 176; be = 256; return true; // Q5_K
     case 14: bb = 210; be = 256; return true; // Q6_K
+    case 11: bb = 110; be = 256; return true; // Q3_K
+    case 23: bb = 136; be = 256; return true; // IQ4_XS
+    case 42: bb = 18; be = 64; return true;   // Q2_0
+    case 142: bb = 34; be = 128; return true; // PQ2_0
     case 30: bb = 2; be = 1; return true;     // BF16
     default: return false;
   }
@@ -255,14 +259,22 @@ int llb_gguf_tensor_at(const llb_gguf* g, uint64_t i, char* name, size_t cap, ui
 // (| format << 28), the shared expert under the dense ffn names (words 3..5); 21 the router, 22 the shared
 // gate row; 26 the expert formats (gate | up << 4 | down << 8, bit 12 fused gate+up, bit 13); 27 experts,
 // 28 expert ff, 29 shared ff, 30 experts used. The nextn (MTP) blocks at the end are left out.
+// The ggml types the table places and their LLB_FM_* codes (host/llb_formats.h:5-14): the reference's
+// writer knows these and BF16 (tools/gguf2pack.c:377-379), but BF16 has no registry entry and its writer
+// does not finish on a file that holds one (its manifest reads the missing entry's code,
+// tools/gguf2pack.c:843,861), so BF16 is refused here.
 static int gg_fm_any(uint32_t ty) {
   switch (ty) {
-    case 0: return 0;   // F32
-    case 1: return 2;   // F16
-    case 8: return 1;   // Q8_0
-    case 12: return 3;  // Q4_K
-    case 13: return 9;  // Q5_K
-    case 14: return 4;  // Q6_K
+    case 0: return 0;    // F32
+    case 1: return 2;    // F16
+    case 8: return 1;    // Q8_0
+    case 12: return 3;   // Q4_K
+    case 13: return 9;   // Q5_K
+    case 14: return 4;   // Q6_K
+    case 11: return 5;   // Q3_K
+    case 42: return 6;   // Q2_0
+    case 142: return 7;  // PQ2_0
+    case 23: return 8;   // IQ4_XS
     default: return -1;
   }
 }
