@@ -12,6 +12,7 @@ A step = one token through the 40 layers; value = microseconds per token-layer.
   python bench.py --traffic-from DIR    (profiles/traffic.json from rocprofv3 FETCH_SIZE / WRITE_SIZE passes)
 """
 import argparse
+import subprocess
 import ctypes as C
 import json
 import os
@@ -36,6 +37,17 @@ def measured_traffic(workload, stage, applies=True):
             return json.load(f)[workload][stage] if applies else None
     except (OSError, KeyError, ValueError):
         return None
+
+
+def traffic_source():
+    """where roofline.traffic comes from: it is not measured in this run (PMC counters need their own
+    rocprofv3 passes), so the line names the file and the commit its passes were made at"""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            at = json.load(f).get("commit", "unrecorded")
+    except (OSError, ValueError):
+        return None
+    return f"profiles/traffic.json (rocprofv3 FETCH_SIZE / WRITE_SIZE passes at commit {at}), not this run"
 
 
 # kernel (rocprofv3 name prefix) -> (workload, stage) for the PMC passes run with --legs prefill,prefill_k;
@@ -87,6 +99,11 @@ def traffic_from(d):
                      "the factors from 256 MiB device-to-device copies (bench.py --copy-calib) profiled the same way",
            "fetch_factor": round(ff, 4), "write_factor": round(wf, 4),
            "calibration_kib": {"fetch": cf, "write": cw}, "kib_per_dispatch": {}}
+    try:
+        out["commit"] = subprocess.run(["git", "-C", ROOT, "rev-parse", "--short", "HEAD"], capture_output=True,
+                                       text=True, timeout=10).stdout.strip() or "unrecorded"
+    except (OSError, subprocess.SubprocessError):
+        out["commit"] = "unrecorded"
     # kernels the passes did not see keep their earlier figures (a pass may cover decode or prefill only)
     try:
         with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
@@ -189,18 +206,26 @@ def prefill(dev, shape, T, layers, steps, warmup, name="", tier=None, graph=Fals
     for L in Ls:
         L.free()
     us_layer = wall / (steps * layers) * 1e6
-    peak = MFMA_F16_PEAK_TFS if tier == em.F16 else MFMA_I8_PEAK_TOPS
-    q8_mfma = os.environ.get("LLB_MOE_Q8_GEMM", "") == "1"
-    kern = ("gate_up GEMM (f16 MFMA)" if tier == em.F16 else
-            "gate_up GEMM (int8 MFMA on q8_1 activations)" if q8_mfma else "gate_up (int8 v_dot4 on q8_1 activations)")
+    q8_mfma = tier != em.F16 and dev.lib.llb_moe_hip_q8_gemm() == 1
+    wgbs = wbytes / (gu_us * 1e-6) / 1e9
+    if tier == em.F16 or q8_mfma:
+        peak = MFMA_F16_PEAK_TFS if tier == em.F16 else MFMA_I8_PEAK_TOPS
+        kern = "gate_up GEMM (f16 MFMA)" if tier == em.F16 else "gate_up GEMM (int8 MFMA on q8_1 activations)"
+        roof = {"bound": "mfma", "kernel": kern, "achieved": round(ach, 1), "peak": peak,
+                "unit": "TFLOP/s" if tier == em.F16 else "TOP/s", "frac": round(ach / peak, 4)}
+    else:
+        # per-slot v_dot4 GEMVs use no matrix core: priced as a weight stream (every expert's gate / up
+        # bytes once a launch) against HBM
+        roof = {"bound": "hbm", "kernel": "gate_up (int8 v_dot4 GEMVs on q8_1 activations, per slot)",
+                "achieved": round(wgbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(wgbs / HBM_PEAK_GBS, 4),
+                "int8_tops": round(ach, 2)}
+    roof.update({"traffic": measured_traffic(f"{name}_prefill_{T}", "gate_up", tier == em.F16),
+                 "traffic_source": traffic_source(),
+                 "kernel_us": round(gu_us, 2), "weight_gbs": round(wgbs, 1)})
     return {"tokens_per_s": round(T / (us_layer * 1e-6), 1), "us_per_layer_chunk": round(us_layer, 2), "T": T,
             "layers": layers, "launch": launch,
             "eager_us_per_layer_chunk": round(wall_eager / (steps * layers) * 1e6, 2),
-            "stages_us": {k: round(v[0], 2) for k, v in st.items()},
-            "roofline": {"bound": "mfma", "kernel": kern, "achieved": round(ach, 1),
-                         "peak": peak, "unit": "TFLOP/s" if tier == em.F16 else "TOP/s", "frac": round(ach / peak, 4),
-                         "traffic": measured_traffic(f"{name}_prefill_{T}", "gate_up", tier == em.F16),
-                         "kernel_us": round(gu_us, 2), "weight_gbs": round(wbytes / (gu_us * 1e-6) / 1e9, 1)}}
+            "stages_us": {k: round(v[0], 2) for k, v in st.items()}, "roofline": roof}
 
 
 def batched(dev, shape, T, layers, steps, warmup, tier):
@@ -583,6 +608,7 @@ def main():
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(f"{args.config}_decode", dom, args.tier == "exact"),
+                     "traffic_source": traffic_source(),
                      "bytes_per_launch": sbytes[dom], "kernel_us": round(dom_us, 3)},
     }
     if step_us is not None:

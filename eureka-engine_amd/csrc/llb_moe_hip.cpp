@@ -15,6 +15,8 @@ int launch_gen_rows(uint32_t fm, uint64_t seed, uint64_t stream, uint64_t r0, ui
 int moe_q8_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const float* x1, float* y, const uint32_t* ids,
                    const float* wt, const float* sgo, const TopkArgs* tk, uint8_t* sc, hipStream_t st);
 size_t moe_q8_scratch(const llb_moe_layer* L, uint32_t T);
+void moe_q8_set_gemm(bool on);
+bool moe_q8_gemm_enabled();
 int launch_group(const uint32_t* ids, uint32_t n, uint32_t nk, uint32_t ne, uint32_t* off, uint32_t* xmap,
                  uint32_t* inv, const float* x, _Float16* x16, uint64_t nx, hipStream_t st);
 int launch_q8_1(const float* x, uint32_t n, int8_t* q, float2* ds, hipStream_t st);
@@ -620,6 +622,11 @@ int llb_moe_hip_set_fused(int on) {
   g_fused = 0;
   return 0;
 }
+int llb_moe_hip_set_q8_gemm(int on) {
+  moe_q8_set_gemm(on != 0);
+  return 0;
+}
+int llb_moe_hip_q8_gemm(void) { return moe_q8_gemm_enabled() ? 1 : 0; }
 int llb_moe_hip_status(llb_dptr scratch, const llb_moe_layer* L, uint32_t T) {
   if (!scratch || !L || !T) return fail(LLB_HIP_EINVAL, "status: null argument");
   const ExactScratch s = exact_layout(L, T);

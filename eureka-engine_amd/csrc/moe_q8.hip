@@ -7,6 +7,7 @@
 
 #include "../../include/llb_moe_hip.h"
 #include "moe_dev.h"
+#include <atomic>
 #include "moe_kernels.h"
 #include "moe_q8dot.h"
 
@@ -230,17 +231,19 @@ static Q8GemmLayout q8_gemm_layout(const llb_moe_layer* L, uint32_t T) {
   g.total = o;
   return g;
 }
-// The int8-MFMA path is switched on by LLB_MOE_Q8_GEMM=1 (read once). It is off by default until it has
-// run on the GPU: its first run faulted (its Q8_0 code loads read 4 bytes past the stack's last block,
-// fixed since), and the fixed code has not run yet. Off, the q8 tier keeps its per-slot kernels at
-// every T.
-static bool q8_gemm_on() {
-  static const int on = [] {
-    const char* e = getenv("LLB_MOE_Q8_GEMM");
-    return e && e[0] == '1' ? 1 : 0;
-  }();
-  return on != 0;
-}
+// The int8-MFMA path is switched by llb_moe_hip_set_q8_gemm (its initial state: LLB_MOE_Q8_GEMM=1 in the
+// environment at load time, else off). It is off by default until it has run on the GPU: its first run
+// faulted (its Q8_0 code loads read 4 bytes past the stack's last block, fixed since), and the fixed code
+// has not run yet. Off, the q8 tier keeps its per-slot kernels at every T. The switch is read at scratch
+// sizing and at each forward; a forward whose scratch was sized with the switch off and that runs with it
+// on is refused by the forward's scratch check.
+static std::atomic<int> g_q8_gemm{[] {
+  const char* e = getenv("LLB_MOE_Q8_GEMM");
+  return e && e[0] == '1' ? 1 : 0;
+}()};
+void moe_q8_set_gemm(bool on) { g_q8_gemm.store(on ? 1 : 0); }
+bool moe_q8_gemm_enabled() { return g_q8_gemm.load() != 0; }
+static bool q8_gemm_on() { return moe_q8_gemm_enabled(); }
 static bool q8_gemm_ok(const llb_moe_layer* L, uint32_t T) {
   const uint32_t fg = L->fx & 15, fu = L->fx >> 4 & 15;
   const uint32_t fd = L->fx >> 8 & 15;

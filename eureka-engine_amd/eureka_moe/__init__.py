@@ -84,6 +84,8 @@ _SIGS = {
                                            C.c_float, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64,
                                            C.c_uint64, C.c_size_t, C.c_int]),
     "llb_moe_hip_set_fused": (C.c_int, [C.c_int]),
+    "llb_moe_hip_set_q8_gemm": (C.c_int, [C.c_int]),
+    "llb_moe_hip_q8_gemm": (C.c_int, []),
     "llb_moe_hip_pack_bytes": (C.c_size_t, [C.POINTER(MoeLayer)]),
     "llb_gguf_open": (C.c_void_p, [C.c_char_p]),
     "llb_gguf_close": (None, [C.c_void_p]),

@@ -158,6 +158,17 @@ int llb_moe_hip_forward_static(const llb_moe_layer* L, uint32_t T, llb_dptr h2, 
  * in a scratch (LLB_HIP_EDEVICE, cleared, when set); with the path disabled it is never set.
  * No counterpart in the reference. */
 int llb_moe_hip_set_fused(int on);
+
+/* The q8 tier from 16 tokens on: the int8-MFMA grouped GEMM (k_gemm_i8, the counterpart of the
+ * reference's int8 tensor-core prefill pfx_* / llb_mx_*, host/llb_pf.cuh:819-848) when on, per-slot v_dot4
+ * GEMVs when off (the same q8_1 numerics class). Off by default: its one GPU run so far faulted, on a cause
+ * since fixed (a Q8_0 code load past the stack's last block) and not yet run again. The initial state comes
+ * from LLB_MOE_Q8_GEMM=1 in the environment at load. The switch sizes the q8 scratch
+ * (llb_moe_hip_scratch_bytes) as well as choosing the kernels: size scratch after setting it, and do not
+ * change it while forwards run. q8_gemm returns the current state. No counterpart in the reference (its
+ * tier is chosen by LLB_PREFILL at build time). */
+int llb_moe_hip_set_q8_gemm(int on);
+int llb_moe_hip_q8_gemm(void);
 int llb_moe_hip_status(llb_dptr scratch, const llb_moe_layer* L, uint32_t T);
 
 /* ---- GGUF expert stacks: llb_moe_load's residency (host/llb_host.c:446-586) and llb_gg_tensor

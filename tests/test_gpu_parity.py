@@ -334,7 +334,8 @@ def test_q8_1_matches_oracle(dev):
     assert np.array_equal(gds[:, 1], rs)  # s: the same xor-butterfly order
 
 
-# T >= 16: the grouped GEMM on int8 MFMA (c2 / c5: with the shared expert; c1k: Q4_K gate / up, Q6_K down)
+# the q8 tier with its default kernels (the int8-MFMA GEMM is off: tests/test_gpu_q8_gemm.py runs it); c2 / c5:
+# with the shared expert; c1k: Q4_K gate / up, Q6_K down
 @pytest.mark.parametrize("name,T", [("c2", 1), ("c1", 4), ("c2", 8), ("c1", 16), ("c2", 40), ("c1k", 100), ("c5", 70)])
 def test_q8_tier_tolerance(dev, name, T):
     shape = em.SHAPES[name]
@@ -360,7 +361,7 @@ def test_q8_tier_tolerance(dev, name, T):
 
 @pytest.mark.parametrize("name", ["c1", "c1k"])
 def test_q8_tier_prefill_2048_sampled(dev, name):
-    """config 4 on the q8 tier (the int8-MFMA grouped GEMM): 2048 tokens, 64 sampled tokens (the first and
+    """config 4 on the q8 tier (its default per-slot kernels): 2048 tokens, 64 sampled tokens (the first and
     last tiles of the most-loaded expert among them) against the oracle's q8 mode"""
     shape, T, seed = em.SHAPES[name], 2048, 6
     _say("q8 prefill", name, "T", T)
