@@ -1322,9 +1322,19 @@ size_t fused_lds(const FusedArgs& f) {
   return m2 > tr ? m2 : tr;
 }
 
+// the fused layer's six counters to zero, by a kernel in the same stream (not a memset: the launch pair may
+// be captured into a graph, where memset nodes have given wrong results on replay)
+__global__ void __launch_bounds__(64) k_fused_clear(u32* c) {
+  if (threadIdx.x < 6) c[threadIdx.x] = 0u;
+}
+
 int launch_fused(const FusedArgs& f, u32 fg, u32 fd, u32 fs, u32 nsp, u32 grid, hipStream_t st) {
   if (nsp != 1) return -1;  // its LDS holds four waves' tree x of one span a lane
   const size_t sm = fused_lds(f);
+  // the counters start at zero at every launch, whatever an earlier call at another T or tier left in
+  // the scratch (the last block out still resets them, which keeps a launch's own end state clean)
+  if (!fused_supported(fg, fd, fs, nsp)) return -1;
+  LAUNCH_K(k_fused_clear, dim3(1), dim3(64), 0, st, f.ctr);
 #define FU_L(FG, FD, FS) \
   if (fg == FG && fd == FD && fs == FS) { \
     if (nsp == 1) { LAUNCH_K((k_fused<FG, FD, FS, 1>), dim3(grid), dim3(256), sm, st, f); return 0; } \

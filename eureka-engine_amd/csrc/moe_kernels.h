@@ -136,7 +136,7 @@ struct FusedArgs {
   uint32_t dpt;  // down items a token
   uint32_t np;   // gate / up row pairs an item
   uint32_t spin; // 100 MHz ticks a wait may take before it records an error
-  uint32_t* ctr; // 6 counters in the scratch, zero between launches
+  uint32_t* ctr; // 6 counters in the scratch, cleared by launch_fused before each launch
 };
 int launch_fused(const FusedArgs& f, uint32_t fg, uint32_t fd, uint32_t fs, uint32_t nsp, uint32_t grid, hipStream_t st);
 bool fused_supported(uint32_t fg, uint32_t fd, uint32_t fs, uint32_t nsp);
