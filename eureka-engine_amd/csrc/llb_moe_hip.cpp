@@ -7,6 +7,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+
 #include "moe_kernels.h"
 
 int launch_gauss(uint64_t seed, uint64_t stream, uint64_t i0, uint64_t n, float sigma, float* out, hipStream_t st);
@@ -17,8 +19,6 @@ int moe_q8_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const fl
 size_t moe_q8_scratch(const llb_moe_layer* L, uint32_t T);
 void moe_q8_set_gemm(bool on);
 bool moe_q8_gemm_enabled();
-int launch_group(const uint32_t* ids, uint32_t n, uint32_t nk, uint32_t ne, uint32_t* off, uint32_t* xmap,
-                 uint32_t* inv, const float* x, _Float16* x16, uint64_t nx, hipStream_t st);
 int launch_q8_1(const float* x, uint32_t n, int8_t* q, float2* ds, hipStream_t st);
 int launch_spin(uint32_t us, hipStream_t st);
 
@@ -326,7 +326,7 @@ static ExactScratch exact_layout(const llb_moe_layer* L, uint32_t T) {
 }
 
 struct GemmScratch {
-  size_t x16, off, xmap, inv, act, out, spill, sact, shd, total;
+  size_t x16, off, xmap, inv, gcnt, act, out, spill, sact, shd, total;
 };
 static GemmScratch gemm_layout(const llb_moe_layer* L, uint32_t T) {
   GemmScratch g;
@@ -336,6 +336,7 @@ static GemmScratch gemm_layout(const llb_moe_layer* L, uint32_t T) {
   g.off = o; o += al(((size_t)L->ne + 1) * 4);
   g.xmap = o; o += al(n * 4);
   g.inv = o; o += al(n * 4);
+  g.gcnt = o; o += al(group_cnt_bytes((uint32_t)n, L->ne));
   g.act = o; o += al(n * L->ef * 2);
   g.out = o; o += al(n * L->dm * 2);
   g.spill = o; o += al(n * L->dm * 4);  // f32 down outputs past f16's range (touched only there)
@@ -463,7 +464,8 @@ static int gemm_forward(const llb_moe_layer* L, uint32_t T, const float* h2, con
   uint32_t* inv = (uint32_t*)(gb + gs.inv);
   _Float16* x16 = (_Float16*)(gb + gs.x16);
   stage_begin(ST_Q8X);
-  if ((rc = launched(launch_group(ids, n, L->nk, L->ne, off, xmap, inv, h2, x16, (uint64_t)T * L->dm, g_stream),
+  if ((rc = launched(launch_group(ids, n, L->nk, L->ne, off, xmap, inv, h2, x16, (uint64_t)T * L->dm, g_stream,
+                                  (uint32_t*)(gb + gs.gcnt)),
                      "group + f16 activations")))
     return rc;
   stage_end(ST_Q8X);
@@ -627,6 +629,14 @@ int llb_moe_hip_set_q8_gemm(int on) {
   return 0;
 }
 int llb_moe_hip_q8_gemm(void) { return moe_q8_gemm_enabled() ? 1 : 0; }
+int llb_moe_hip_set_group_scan(int on) {
+  moe_set_group_scan(on != 0);
+  return 0;
+}
+int llb_moe_hip_group_scan(void) { return moe_group_scan_enabled() ? 1 : 0; }
+size_t llb_moe_hip_group_scratch_bytes(uint32_t n, uint32_t ne) {
+  return std::max((size_t)(ne + 1) * 4, group_cnt_bytes(n, ne));
+}
 int llb_moe_hip_status(llb_dptr scratch, const llb_moe_layer* L, uint32_t T) {
   if (!scratch || !L || !T) return fail(LLB_HIP_EINVAL, "status: null argument");
   const ExactScratch s = exact_layout(L, T);
@@ -972,9 +982,11 @@ int llb_moe_hip_topk(llb_dptr lg, uint32_t lstride, uint32_t T, uint32_t ne, uin
 int llb_moe_hip_group(llb_dptr ids, uint32_t n, uint32_t nk, uint32_t ne, llb_dptr off, llb_dptr xmap, llb_dptr inv,
                       llb_dptr scratch, size_t scratch_bytes) {
   if (!ne || !nk || n % nk) return fail(LLB_HIP_EINVAL, "group: n must be a multiple of nk");
-  if (scratch_bytes < (size_t)(ne + 1) * 4) return fail(LLB_HIP_ESCRATCH, "group: scratch < (ne + 1) * 4 bytes");
+  // (the per-expert scans need no scratch; (ne + 1) * 4 bytes has always been asked)
+  const size_t need = moe_group_scan_enabled() ? llb_moe_hip_group_scratch_bytes(n, ne) : (size_t)(ne + 1) * 4;
+  if (scratch_bytes < need) return fail(LLB_HIP_ESCRATCH, "group: scratch < %zu bytes", need);
   return launched(launch_group(dp<uint32_t>(ids), n, nk, ne, dp<uint32_t>(off), dp<uint32_t>(xmap), dp<uint32_t>(inv),
-                               nullptr, nullptr, 0, g_stream),
+                               nullptr, nullptr, 0, g_stream, dp<uint32_t>(scratch)),
                   "group");
 }
 

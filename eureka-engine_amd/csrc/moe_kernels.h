@@ -204,8 +204,13 @@ struct GemmQ8Args {
 int launch_gemm_i8(const GemmQ8Args& g, uint32_t fm, uint32_t mode, uint32_t grid_y, hipStream_t st);
 int launch_combine_f32(const float* out, const uint32_t* inv, const float* wt, uint32_t nk, const float* shd,
                        const float* sgo, const float* x1, float* y, uint32_t dm, uint32_t T, hipStream_t st);
+// cnt: group_cnt_bytes(n, ne) of scratch for the histogram + scan pair (used when it is switched on;
+// null keeps k_group)
 int launch_group(const uint32_t* ids, uint32_t n, uint32_t nk, uint32_t ne, uint32_t* off, uint32_t* xmap,
-                 uint32_t* inv, const float* x, _Float16* x16, uint64_t nx, hipStream_t st);
+                 uint32_t* inv, const float* x, _Float16* x16, uint64_t nx, hipStream_t st, uint32_t* cnt);
+size_t group_cnt_bytes(uint32_t n, uint32_t ne);
+void moe_set_group_scan(bool on);
+bool moe_group_scan_enabled();
 int launch_q8_1(const float* x, uint32_t n, int8_t* q, float2* ds, hipStream_t st);
 uint32_t gemm_bm();
 int llb_fail_msg(int code, const char* msg);  // sets llb_hip_last_error's text, returns code

@@ -135,10 +135,161 @@ __global__ void __launch_bounds__(256) k_group(const u32* __restrict__ ids, u32 
   }
 }
 
+// ---- the same permutation as a device histogram and prefix scan (two launches, O(n + nb ne) work)
+//
+// Slot i lives in block b = i / GS_SLOTS, wave w = (i % GS_SLOTS) / 256, round r = (i % 256) / 64, lane
+// L = i % 64, so (b, w, r, L) ascending is slot order. k_group_count: within each round a wave gives every
+// lane its rank among the round's lanes of the same expert (lanes below it, by ballot: one pass per
+// distinct expert in the round, leader = the lowest lane left) plus the wave's running count of that expert
+// (LDS, wave-private); after the four rounds the block turns its per-wave counts into per-wave exclusive
+// prefixes, writes its per-expert totals cnt[b][e] and each slot's rank inside the block into inv[i].
+// k_group_place: every block sums cnt over blocks for its experts (those before it, and all), scans the
+// totals over experts (off[e] = slots with id < e), and places its slots: pos = off[e] + (slots of e in
+// earlier blocks) + rank, xmap[pos] = i / nk, inv[i] = pos. Ids >= ne (never produced by routing) get no
+// position, as in k_group. Blocks past nb convert the activations to f16 as k_group's do.
+constexpr u32 GS_SLOTS = 1024;
+__global__ void __launch_bounds__(256) k_group_count(const u32* __restrict__ ids, u32 n, u32 ne, u32* __restrict__ cnt,
+                                                     u32* __restrict__ inv) {
+  extern __shared__ u32 wc[];  // [4][ne]
+  const u32 t = threadIdx.x, L = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6);
+  for (u32 i = t; i < 4 * ne; i += 256) wc[i] = 0u;
+  __syncthreads();
+  u32* mine = wc + w * ne;
+  const u32 s0 = blockIdx.x * GS_SLOTS + w * 256;
+  const u64 below = L ? (~0ull >> (64 - L)) : 0ull;  // lanes under this one
+  u32 rk[4], ev[4];
+#pragma unroll
+  for (u32 r = 0; r < 4; r++) {
+    const u32 i = s0 + 64 * r + L;
+    const u32 e = i < n ? ids[i] : 0xFFFFFFFFu;
+    const bool ok = e < ne;
+    u64 act = __ballot(ok);
+    u32 my = 0;
+    while (act) {  // wave-uniform: one pass per distinct expert of the round
+      const u32 ld = (u32)__builtin_ctzll(act);
+      const u32 ee = (u32)__builtin_amdgcn_readlane((int)e, (int)ld);
+      const bool same = ok && e == ee;
+      const u64 m = __ballot(same);
+      const u32 base = mine[ee];
+      if (same) my = base + (u32)__builtin_popcountll(m & below);
+      if (L == ld) mine[ee] = base + (u32)__builtin_popcountll(m);
+      // the next pass (or round) may read this count: keep the LDS store ahead of it
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      act &= ~m;
+    }
+    rk[r] = my;
+    ev[r] = ok ? e : 0xFFFFFFFFu;
+  }
+  __syncthreads();
+  for (u32 e = t; e < ne; e += 256) {
+    const u32 a0 = wc[e], a1 = wc[ne + e], a2 = wc[2 * ne + e], a3 = wc[3 * ne + e];
+    wc[e] = 0u;
+    wc[ne + e] = a0;
+    wc[2 * ne + e] = a0 + a1;
+    wc[3 * ne + e] = a0 + a1 + a2;
+    cnt[(u64)blockIdx.x * ne + e] = a0 + a1 + a2 + a3;
+  }
+  __syncthreads();
+#pragma unroll
+  for (u32 r = 0; r < 4; r++) {
+    const u32 i = s0 + 64 * r + L;
+    if (ev[r] != 0xFFFFFFFFu) inv[i] = mine[ev[r]] + rk[r];
+  }
+}
+
+__global__ void __launch_bounds__(256) k_group_place(const u32* __restrict__ ids, u32 n, u32 nk, u32 ne, u32 nb,
+                                                     const u32* __restrict__ cnt, u32* __restrict__ off,
+                                                     u32* __restrict__ xmap, u32* __restrict__ inv,
+                                                     const float* __restrict__ x, _Float16* __restrict__ x16, u64 nx) {
+  __shared__ u32 base[1024];
+  __shared__ u32 wsum[4];
+  if (blockIdx.x >= nb) {
+    const u64 i = ((u64)(blockIdx.x - nb) * 256 + threadIdx.x) * 8;
+    if (i < nx) {
+      const float4 a = *(const float4*)(x + i), b = *(const float4*)(x + i + 4);
+      typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+      const h8 v = {(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+                    (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
+      *(h8*)(x16 + i) = v;
+    }
+    return;
+  }
+  const u32 t = threadIdx.x, L = t & 63, w = t >> 6, b = blockIdx.x;
+  // thread t: experts 4 t .. 4 t + 3 (ne <= 1024), each summed over the blocks before this one and over all
+  u32 tot[4], bef[4], own = 0;
+#pragma unroll
+  for (u32 j = 0; j < 4; j++) {
+    const u32 e = 4 * t + j;
+    u32 a = 0, c = 0;
+    if (e < ne)
+      for (u32 k = 0; k < nb; k++) {
+        const u32 v = cnt[(u64)k * ne + e];
+        a += k < b ? v : 0u;
+        c += v;
+      }
+    bef[j] = a;
+    tot[j] = c;
+    own += c;
+  }
+  // exclusive scan of the threads' totals (expert order): within the wave, then the waves before
+  u32 inc = own;
+#pragma unroll
+  for (u32 m = 1; m < 64; m <<= 1) {
+    const u32 o = __shfl_up(inc, m, 64);
+    if (L >= m) inc += o;
+  }
+  if (L == 63) wsum[w] = inc;
+  __syncthreads();
+  u32 pre = inc - own;
+  for (u32 k = 0; k < w; k++) pre += wsum[k];
+#pragma unroll
+  for (u32 j = 0; j < 4; j++) {
+    const u32 e = 4 * t + j;
+    if (e < ne) {
+      base[e] = pre + bef[j];
+      if (b == 0) off[e] = pre;
+    }
+    pre += tot[j];
+  }
+  if (b == 0 && t == 0) off[ne] = n;
+  __syncthreads();
+  const u32 s0 = b * GS_SLOTS;
+#pragma unroll
+  for (u32 q = 0; q < 4; q++) {
+    const u32 i = s0 + 256 * q + t;
+    if (i < n) {
+      const u32 e = ids[i];
+      if (e < ne) {
+        const u32 pos = base[e] + inv[i];
+        inv[i] = pos;
+        xmap[pos] = i / nk;
+      }
+    }
+  }
+}
+
+// the permutation's choice: 0 k_group (per-expert scans), 1 the histogram + scan pair. Off (0) by default
+// until the pair has run on the GPU.
+static std::atomic<int> g_group_scan{0};
+void moe_set_group_scan(bool on) { g_group_scan.store(on ? 1 : 0); }
+bool moe_group_scan_enabled() { return g_group_scan.load() != 0; }
+size_t group_cnt_bytes(uint32_t n, uint32_t ne) {
+  return (size_t)((n + GS_SLOTS - 1) / GS_SLOTS) * ne * 4;
+}
+
 int launch_group(const uint32_t* ids, uint32_t n, uint32_t nk, uint32_t ne, uint32_t* off, uint32_t* xmap,
-                 uint32_t* inv, const float* x, _Float16* x16, uint64_t nx, hipStream_t st) {
+                 uint32_t* inv, const float* x, _Float16* x16, uint64_t nx, hipStream_t st, uint32_t* cnt) {
   if (x16 && nx % 8) return -1;
   const u64 nconv = x16 ? (nx + 2047) / 2048 : 0;
+  if (cnt && n && ne <= 1024 && moe_group_scan_enabled()) {  // (no slots: k_group writes the all-zero offsets)
+    const u32 nb = (n + GS_SLOTS - 1) / GS_SLOTS;
+    if (nb + nconv > 0x7fffffffull) return -1;
+    hipLaunchKernelGGL(k_group_count, dim3(nb), dim3(256), 4 * ne * 4, st, ids, n, ne, cnt, inv);
+    hipLaunchKernelGGL(k_group_place, dim3((u32)(nb + nconv)), dim3(256), 0, st, ids, n, nk, ne, nb, cnt, off, xmap,
+                       inv, x, x16, nx);
+    return 0;
+  }
   if (ne + nconv > 0x7fffffffull) return -1;
   hipLaunchKernelGGL(k_group, dim3((u32)(ne + nconv)), dim3(256), 0, st, ids, n, nk, ne, off, xmap, inv, x, x16, nx);
   return 0;
@@ -209,7 +360,7 @@ static uint64_t rbytes(uint32_t fm, uint32_t cols) {
 // many tokens: the grouped GEMM path on int8 MFMA (moe_q8_gemm below)
 #define Q8_GEMM_T 16u
 struct Q8GemmLayout {
-  size_t hq, hd, off, xmap, inv, act, aq, ad, out, sa, sq, sd, shd, total;
+  size_t hq, hd, off, xmap, inv, gcnt, act, aq, ad, out, sa, sq, sd, shd, total;
 };
 static Q8GemmLayout q8_gemm_layout(const llb_moe_layer* L, uint32_t T) {
   Q8GemmLayout g;
@@ -220,6 +371,7 @@ static Q8GemmLayout q8_gemm_layout(const llb_moe_layer* L, uint32_t T) {
   g.off = o; o += al(((size_t)L->ne + 1) * 4);
   g.xmap = o; o += al(n * 4);
   g.inv = o; o += al(n * 4);
+  g.gcnt = o; o += al(group_cnt_bytes((uint32_t)n, L->ne));
   g.act = o; o += al(n * L->ef * 4);
   g.aq = o; o += al(n * L->ef);
   g.ad = o; o += al(n * L->ef / 32 * 8);
@@ -281,7 +433,7 @@ static int moe_q8_gemm(const llb_moe_layer* L, uint32_t T, const float* h2, cons
   const uint64_t rbg = rbytes(fg, L->dm), rbd = rbytes(fd, L->ef);
   stage_begin(ST_Q8X);
   int rc = launch_q8_1(h2, T * L->dm, hq, hd, st);
-  if (!rc) rc = launch_group(ids, n, L->nk, L->ne, off, xmap, inv, nullptr, nullptr, 0, st);
+  if (!rc) rc = launch_group(ids, n, L->nk, L->ne, off, xmap, inv, nullptr, nullptr, 0, st, (uint32_t*)(sc + q.gcnt));
   stage_end(ST_Q8X);
   if (rc) return rc;
   const uint32_t maxt = n / gemm_bm() + L->ne + 1;  // >= sum over experts of ceil(M_e / 64)

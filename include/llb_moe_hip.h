@@ -231,9 +231,18 @@ int llb_moe_hip_rmsnorm_add(llb_dptr x, llb_dptr z, llb_dptr w, float eps, uint3
  * then the shared gate's at index ne when has_sg) -> ids, wt [T][nk], sgo [T] */
 int llb_moe_hip_topk(llb_dptr lg, uint32_t lstride, uint32_t T, uint32_t ne, uint32_t nk, uint32_t has_sg,
                      llb_dptr ids, llb_dptr wt, llb_dptr sgo);
-/* llb_mx_group (host/llb_pf.cuh:774-817): n = T nk slots -> off [ne+1], xmap [n], inv [n] */
+/* llb_mx_group (host/llb_pf.cuh:774-817): n = T nk slots -> off [ne+1], xmap [n], inv [n]. scratch:
+ * group_scratch_bytes(n, ne) bytes (the histogram + scan pair's per-block expert counts). */
 int llb_moe_hip_group(llb_dptr ids, uint32_t n, uint32_t nk, uint32_t ne, llb_dptr off, llb_dptr xmap, llb_dptr inv,
                       llb_dptr scratch, size_t scratch_bytes);
+size_t llb_moe_hip_group_scratch_bytes(uint32_t n, uint32_t ne);
+/* The dispatch permutation's kernels: off (the default), one block an expert scanning every slot (O(ne n));
+ * on, a device histogram and prefix scan (two launches, O(n + ne n / 1024), ne <= 1024): per-block stable
+ * counts by wave ballots, then per-expert offsets by a scan over blocks and experts, then placement. Both
+ * give the same off / xmap / inv (the stable order). The scan pair is off until it has run on a GPU.
+ * No counterpart in the reference (llb_mx_group is one fixed kernel). */
+int llb_moe_hip_set_group_scan(int on);
+int llb_moe_hip_group_scan(void);
 /* pf_q8x (tools/pf27/pfmm.cuh:39-54): n f32 (n % 32 == 0) -> q int8 [n], ds float2 {d, s} [n / 32] */
 int llb_moe_hip_q8_1(llb_dptr x, uint32_t n, llb_dptr q, llb_dptr ds);
 /* rows of a stack dequantized to f32 (the decoders the kernels use; q8g_w / q4k_w / q6k_w / q5k_w) */

@@ -307,8 +307,9 @@ def test_group_matches_stable_sort(dev, T, nk, ne):
     ids = np.stack([rng.permutation(ne)[:nk] for _ in range(T)]).astype(np.uint32).ravel()
     n = ids.size
     pi = dev.upload(ids)
-    off, xm, inv, sc = dev.alloc((ne + 1) * 4), dev.alloc(n * 4), dev.alloc(n * 4), dev.alloc((ne + 1) * 4)
-    dev.check(dev.lib.llb_moe_hip_group(pi, n, nk, ne, off, xm, inv, sc, (ne + 1) * 4))
+    sb = dev.lib.llb_moe_hip_group_scratch_bytes(n, ne)
+    off, xm, inv, sc = dev.alloc((ne + 1) * 4), dev.alloc(n * 4), dev.alloc(n * 4), dev.alloc(sb)
+    dev.check(dev.lib.llb_moe_hip_group(pi, n, nk, ne, off, xm, inv, sc, sb))
     go = dev.read(off, ne + 1, np.uint32)
     gx = dev.read(xm, n, np.uint32)
     gv = dev.read(inv, n, np.uint32)
