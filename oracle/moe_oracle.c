@@ -259,17 +259,25 @@ float mo_gauss(u64 seed, u64 stream, u64 i, float sigma) {
 void mo_gauss_fill(u64 seed, u64 stream, u64 i0, u64 n, float sigma, float* out) {
   for (u64 i = 0; i < n; i++) out[i] = mo_gauss(seed, stream, i0 + i, sigma);
 }
+/* rows are independent: split over OpenMP threads (each row's bytes depend only on its own index) */
 int mo_gen_rows(u32 fm, u64 seed, u64 stream, u64 r0, u64 nr, u32 cols, float sigma, u8* out) {
   const u64 rb = mo_row_bytes(fm, cols);
   if (rb == 0) return -1;
-  float* x = (float*)malloc((size_t)cols * 4);
-  if (!x) return -2;
   int rc = 0;
-  for (u64 r = 0; r < nr && rc == 0; r++) {
-    mo_gauss_fill(seed, stream, (r0 + r) * cols, cols, sigma, x);
-    rc = mo_quant_row(fm, x, cols, out + r * rb);
+#pragma omp parallel if (nr >= 64)
+  {
+    float* x = (float*)malloc((size_t)cols * 4);
+    int mine = x ? 0 : -2;
+#pragma omp for schedule(static)
+    for (long long r = 0; r < (long long)nr; r++) {
+      if (mine) continue;
+      mo_gauss_fill(seed, stream, (r0 + (u64)r) * cols, cols, sigma, x);
+      mine = mo_quant_row(fm, x, cols, out + (u64)r * rb);
+    }
+#pragma omp critical
+    if (mine && !rc) rc = mine;
+    free(x);
   }
-  free(x);
   return rc;
 }
 

@@ -169,9 +169,11 @@ class HostLayer:
         s, L = self.shape, self.layer * 16
         rbg, rbu, rbd = row_bytes(s.fg, s.dm), row_bytes(s.fu, s.dm), row_bytes(s.fd, s.ef)
         for e in sorted(set(int(x) for x in experts) - self.have):
-            self.G[e * s.ef * rbg:(e + 1) * s.ef * rbg] = gen_rows(s.fg, self.seed, L + ST_G, e * s.ef, s.ef, s.dm)
-            self.U[e * s.ef * rbu:(e + 1) * s.ef * rbu] = gen_rows(s.fu, self.seed, L + ST_U, e * s.ef, s.ef, s.dm)
-            self.D[e * s.dm * rbd:(e + 1) * s.dm * rbd] = gen_rows(s.fd, self.seed, L + ST_D, e * s.dm, s.dm, s.ef)
+            # generated in place (the rows of expert e of each stack)
+            for buf, fm, st, nr, cols, rb in ((self.G, s.fg, ST_G, s.ef, s.dm, rbg), (self.U, s.fu, ST_U, s.ef, s.dm, rbu),
+                                              (self.D, s.fd, ST_D, s.dm, s.ef, rbd)):
+                assert lib().mo_gen_rows(fm, self.seed, L + st, e * nr, nr, cols, W_SIGMA,
+                                         buf.ctypes.data + e * nr * rb) == 0
             self.have.add(e)
 
     def _mk(self):

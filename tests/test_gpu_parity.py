@@ -361,9 +361,9 @@ def test_q8_tier_tolerance(dev, name, T):
 
 
 @pytest.mark.parametrize("name", ["c1", "c1k"])
-def test_q8_tier_prefill_2048_sampled(dev, name):
-    """config 4 on the q8 tier (its default per-slot kernels): 2048 tokens, 64 sampled tokens (the first and
-    last tiles of the most-loaded expert among them) against the oracle's q8 mode"""
+def test_q8_tier_prefill_2048(dev, name):
+    """config 4 on the q8 tier (its default per-slot kernels): 2048 tokens, every token against the oracle's
+    q8 mode (routing bit-exact)"""
     shape, T, seed = em.SHAPES[name], 2048, 6
     _say("q8 prefill", name, "T", T)
     layer = em.Layer(dev, shape, seed=seed)
@@ -373,12 +373,10 @@ def test_q8_tier_prefill_2048_sampled(dev, name):
     y, ids, wt = run.outputs()
     run.free()
     layer.free()
-    toks, big, mine = _sample_tokens(ids, T, seed)
     h2, _ = ol.inputs(shape, seed, T)
-    yq, idq, wtq, _ = ol.HostLayer(shape, seed=seed, experts=[]).run(h2[toks], None, tier="q8",
-                                                                    nthreads=ORACLE_THREADS)
-    assert np.array_equal(ids[toks], idq) and np.array_equal(wt[toks].view(np.uint32), wtq.view(np.uint32))
-    m = ol.err_metrics(y[toks], yq)
+    yq, idq, wtq, _ = ol.HostLayer(shape, seed=seed, experts=[]).run(h2, None, tier="q8", nthreads=ORACLE_THREADS)
+    assert np.array_equal(ids, idq) and np.array_equal(wt.view(np.uint32), wtq.view(np.uint32))
+    m = ol.err_metrics(y, yq)
     _say("q8 prefill vs oracle q8", m)
     assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
 
@@ -566,27 +564,10 @@ def test_dequant_every_f16_scale(dev):
     dev.free(out)
 
 
-def _sample_tokens(ids, T, seed, n=64):
-    """n tokens to check against the oracle: the first 16 and the last 16 tokens routed to the expert with
-    the most slots (the first and last 64-slot tiles of its GEMM: slots are ordered by token within an
-    expert), token 0 and T - 1, then random others"""
-    flat = ids.ravel()
-    big = int(np.bincount(flat, minlength=int(flat.max()) + 1).argmax())
-    mine = np.nonzero((ids == big).any(axis=1))[0]
-    pick = list(dict.fromkeys([0, T - 1] + mine[:16].tolist() + mine[-16:].tolist()))
-    rest = np.random.default_rng(seed).permutation(T)
-    for t in rest:
-        if len(pick) >= min(n, T):
-            break
-        if int(t) not in pick:
-            pick.append(int(t))
-    return np.array(sorted(pick)), big, mine
-
-
 ORACLE_THREADS = min(16, os.cpu_count() or 1)
 
 
-def _f16_case(dev, name, T, seed, sample=None, bias=None):
+def _f16_case(dev, name, T, seed, bias=None):
     shape = em.SHAPES[name]
     _say("f16 tier", name, "T", T, "seed", seed)
     layer = em.Layer(dev, shape, seed=seed, bias=bias)
@@ -597,17 +578,11 @@ def _f16_case(dev, name, T, seed, sample=None, bias=None):
     run.free()
     layer.free()
     h2, _ = ol.inputs(shape, seed, T)
-    if sample is None:
-        toks = np.arange(T)
-    else:
-        toks, big, mine = _sample_tokens(ids, T, seed, sample)
-        assert len(toks) >= sample and set(mine[:16]) <= set(toks) and set(mine[-16:]) <= set(toks)
-        _say("sampled", len(toks), "tokens; largest expert", big, "with", len(mine), "slots")
     hl = ol.HostLayer(shape, seed=seed, experts=[], bias=bias)
-    yr, idr, wtr, _ = hl.run(h2[toks], None, nthreads=ORACLE_THREADS)
-    assert np.array_equal(ids[toks], idr)  # routing is the exact tier's at every tier
-    assert np.array_equal(wt[toks].view(np.uint32), wtr.view(np.uint32))
-    m = ol.err_metrics(y[toks], yr)
+    yr, idr, wtr, _ = hl.run(h2, None, nthreads=ORACLE_THREADS)
+    assert np.array_equal(ids, idr)  # routing is the exact tier's at every tier
+    assert np.array_equal(wt.view(np.uint32), wtr.view(np.uint32))
+    m = ol.err_metrics(y, yr)
     _say("f16 tier vs exact oracle", m)
     return m
 
@@ -619,19 +594,18 @@ def test_f16_tier_tolerance(dev, name, T):
 
 
 @pytest.mark.parametrize("name", ["c1", "c1k"])
-def test_f16_tier_prefill_2048_sampled(dev, name):
-    """config 4: 2048 tokens through the config-1 layer (Q8_0) and its Q4_K / Q6_K variant; 64 tokens
-    checked against the oracle, among them the first and last tiles of the most-loaded expert"""
-    m = _f16_case(dev, name, 2048, seed=0, sample=64)
+def test_f16_tier_prefill_2048(dev, name):
+    """config 4: 2048 tokens through the config-1 layer (Q8_0) and its Q4_K / Q6_K variant; every token
+    checked against the oracle (routing bit-exact)"""
+    m = _f16_case(dev, name, 2048, seed=0)
     assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
 
 
 def test_f16_tier_config5_mixed(dev):
     """config 5: 512 experts top-10 with the shared expert, one decode token plus a 512-token chunk in one
-    launch, Zipf(1.1) router bias; 64 tokens (token 0, the first and last tiles of the most-loaded expert)
-    checked against the oracle (routing bit-exact)"""
+    launch, Zipf(1.1) router bias; every token checked against the oracle (routing bit-exact)"""
     shape, seed = em.SHAPES["c5"], 5
-    m = _f16_case(dev, "c5", 513, seed=seed, sample=64, bias=em.zipf_bias(shape.ne, seed))
+    m = _f16_case(dev, "c5", 513, seed=seed, bias=em.zipf_bias(shape.ne, seed))
     assert m["max_rel"] < 2e-3 and m["cos"] >= 0.9999, m
 
 
