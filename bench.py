@@ -427,6 +427,9 @@ def main():
     ap.add_argument("--config", default="c2")
     ap.add_argument("--tier", default="exact", choices=["exact", "q8"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--q8-gemm", action="store_true", help="the q8 tier's int8-MFMA GEMM (llb_moe_hip_set_q8_gemm)")
+    ap.add_argument("--group-scan", action="store_true", help="histogram + scan dispatch (llb_moe_hip_set_group_scan)")
+    ap.add_argument("--lean-topk", action="store_true", help="the decode's lean top-k (llb_moe_hip_set_lean_topk)")
     ap.add_argument("--eager", dest="graph", action="store_false", help="launch per layer instead of a graph")
     ap.add_argument("--no-prefill", dest="prefill", action="store_false", help="skip the prefill leg")
     ap.add_argument("--prefill-config", default="c1")
@@ -469,6 +472,9 @@ def main():
     shape = em.SHAPES[args.config]
     tier = em.EXACT if args.tier == "exact" else em.Q8
     dev = em.Device(0)
+    dev.check(dev.lib.llb_moe_hip_set_q8_gemm(1 if args.q8_gemm else 0))
+    dev.check(dev.lib.llb_moe_hip_set_group_scan(1 if args.group_scan else 0))
+    dev.check(dev.lib.llb_moe_hip_set_lean_topk(1 if args.lean_topk else 0))
     layers = [em.Layer(dev, shape, seed=0, layer=i) for i in range(args.layers)]
     T = 1
     h2 = dev.alloc(args.layers * shape.dm * 4)
@@ -598,6 +604,7 @@ def main():
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32" if tier == em.EXACT else "int8",
         "data": "synthetic: weights N(0,0.02) quantized on the device by this project's quantizers, x N(0,1)",
+        "variants": {"q8_gemm": args.q8_gemm, "group_scan": args.group_scan, "lean_topk": args.lean_topk},
         "config": {"workload": f"{args.config} decode, 1 token through {args.layers} resident layers, {args.tier} tier"
                                 f"{', one HIP graph a step' if args.graph else ', eager launches'}",
                    "dm": shape.dm, "ne": shape.ne, "nk": shape.nk, "ef": shape.ef, "sf": shape.sf,

@@ -8,6 +8,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include "moe_kernels.h"
 
@@ -616,6 +617,8 @@ int llb_moe_hip_pack(llb_moe_layer* L, llb_dptr buf, size_t bytes) {
 // the fused one-launch layer (exact tier, small T). It hung the GPU twice and the cause is not
 // shown, so it stays off: asking for it is refused; 0 (the four-launch path) is accepted.
 static int g_fused = 0;
+// the one-token decode's top-k variant (topk_block4 when set); off until it has run on a GPU
+static std::atomic<int> g_lean_topk{0};
 static int g_ncu = 0;
 int llb_moe_hip_set_fused(int on) {
   if (on)
@@ -629,6 +632,11 @@ int llb_moe_hip_set_q8_gemm(int on) {
   return 0;
 }
 int llb_moe_hip_q8_gemm(void) { return moe_q8_gemm_enabled() ? 1 : 0; }
+int llb_moe_hip_set_lean_topk(int on) {
+  g_lean_topk.store(on ? 1 : 0);
+  return 0;
+}
+int llb_moe_hip_lean_topk(void) { return g_lean_topk.load(); }
 int llb_moe_hip_set_group_scan(int on) {
   moe_set_group_scan(on != 0);
   return 0;
@@ -729,6 +737,7 @@ static int decode_forward(const llb_moe_layer* L, const float* h2, const float* 
   g.SD = L->sf ? dp<uint8_t>(L->SD) : nullptr;
   g.rbs = L->sf ? row_bytes(L->fsd, L->sf) : 0;
   g.ndb = (L->dm + 7) / 8;
+  g.lean = g_lean_topk.load() ? 1u : 0u;
 #ifdef MOE_DEC_STAMPS
   g.stamps = g_dec_stamps;
 #endif

@@ -446,6 +446,76 @@ DEV TopkLane topk_block(const float* lg, u32 ne, u32 nk, u8* tl, float* xs, floa
   return out;
 }
 
+// The same routing for ne <= 256 with four barriers instead of seven (selected by DecGuArgs::lean).
+// Expert e on thread e (waves 0..3 hold the four 64-expert groups); max and group sums as topk_block.
+// A key's place in its group is counted in registers: lane L compares its key with the 64 keys of its
+// wave read one lane at a time (readlane), no LDS and no barrier. Places below nc = min(nk, 16) go to
+// LDS as candidates (other places: key 0, below every real key). Wave 0 then ranks the 64 candidate
+// slots (lane g 16 + q: group g's place q) by counting larger candidates among all 64, again by
+// readlane; ranks below nk with a real p name the slots. Same keys, same order, same results as
+// topk_block. LDS: the candidates at topk_block's candidate offset, red and the slots at its offsets.
+DEV TopkLane topk_block4(const float* lg, u32 ne, u32 nk, u8* tl, float* xs, float4 xv) {
+  unsigned long long* cand = (unsigned long long*)tl + 512;  // [4][16]
+  float* red = (float*)(tl + 512 * 8 + 128 * 8 + 1024);
+  u32* sid = (u32*)(red + 64);
+  float* sp = (float*)(sid + 64);
+  const u32 t = threadIdx.x, L = t & 63, w = t >> 6;
+  const u32 nc = min(nk, 16u);
+  float v = 0.0f;
+  if (t < 256) {
+    v = t < ne ? lg[t] : 0.0f;
+    const float mw = wave_fmax(t < ne ? v : bits_f(0xFF800000u));
+    if (L == 0) red[w] = mw;
+  }
+  if (t < 64) { sid[t] = 0u; sp[t] = 0.0f; }
+  __syncthreads();
+  if (t < 512) *(float4*)(xs + xpad(4 * t)) = xv;
+  float mx = red[0];
+#pragma unroll
+  for (u32 i = 1; i < 4; i++) mx = fmaxf(mx, red[i]);
+  if (t < 256) {
+    v = t < ne ? exp_f(v - mx) : 0.0f;
+    const float sg = tree32_desc(v);
+    if ((L & 31) == 0) red[16 + (t >> 5)] = sg;
+  }
+  __syncthreads();
+  if (t < 256) {
+    float tot = 0.0f;
+#pragma unroll
+    for (u32 g = 0; g < 8; g++) tot = tot + red[16 + g];
+    const float p = v * (1.0f / tot);
+    const u32 kb = (t < ne && p >= 0.0f) ? __float_as_uint(p) + 1u : 0u;
+    const u32 klo = 0xFFFFFFFFu - t;
+    u32 place = 0;
+#pragma unroll
+    for (u32 i = 0; i < 64; i++) {
+      const u32 hi = (u32)__builtin_amdgcn_readlane((int)kb, (int)i), lo = (u32)__builtin_amdgcn_readlane((int)klo, (int)i);
+      place += (hi > kb || (hi == kb && lo > klo)) ? 1u : 0u;
+    }
+    if (place < nc) cand[w * 16 + place] = ((u64)kb << 32) | klo;
+    if (L < 16 && L >= nc) cand[w * 16 + L] = 0ull;
+  }
+  __syncthreads();
+  if (t < 64) {
+    const u64 mine = cand[t];
+    const u32 mh = (u32)(mine >> 32), ml = (u32)mine;
+    u32 rk = 0;
+#pragma unroll
+    for (u32 i = 0; i < 64; i++) {
+      const u32 hi = (u32)__builtin_amdgcn_readlane((int)mh, (int)i), lo = (u32)__builtin_amdgcn_readlane((int)ml, (int)i);
+      rk += (hi > mh || (hi == mh && lo > ml)) ? 1u : 0u;
+    }
+    if ((t & 15) < nc && rk < nk && mh != 0u) {
+      sid[rk] = 0xFFFFFFFFu - ml;
+      sp[rk] = __uint_as_float(mh - 1u);
+    }
+  }
+  __syncthreads();
+  TopkLane out{0u, 0.0f};
+  if (t < 64) { out.id = sid[t]; out.p = sp[t]; }
+  return out;
+}
+
 // wt_j = p_j / max(sum of the nk p in rank order, 2^-14) on lane j
 DEV float topk_renorm(const TopkLane& t, u32 nk) {
   float s = 0.0f;
@@ -699,11 +769,15 @@ __global__ void __launch_bounds__(1024) k_gu_dec(DecGuArgs a) {
   if constexpr (NI <= 8) {
     if (a.tk.nk <= 16) {  // the routing by the whole block; x goes to LDS on the way; its last barrier
                           // publishes the slots
+      if (NI == 4 && a.lean) {
+        tl = topk_block4(a.tk.lg, a.tk.ne, a.tk.nk, tkb, xs, xv);
+      } else {
 #ifdef MOE_DEC_STAMPS
-      tl = topk_block<64 * NI>(a.tk.lg, a.tk.ne, a.tk.nk, tkb, xs, xv, a.stamps);
+        tl = topk_block<64 * NI>(a.tk.lg, a.tk.ne, a.tk.nk, tkb, xs, xv, a.stamps);
 #else
-      tl = topk_block<64 * NI>(a.tk.lg, a.tk.ne, a.tk.nk, tkb, xs, xv);
+        tl = topk_block<64 * NI>(a.tk.lg, a.tk.ne, a.tk.nk, tkb, xs, xv);
 #endif
+      }
       ids_s = (const u32*)(tkb + 512 * 8 + 128 * 8 + 1024 + 64 * 4);
       routed_ok = true;
     }

@@ -94,6 +94,7 @@ struct DecGuArgs {
   const uint8_t* SD;
   uint64_t rbs;
   uint32_t ndb;           // down blocks (DN_RB outputs each)
+  uint32_t lean;          // 1: top-k by topk_block4 (ne <= 256, four barriers)
 #ifdef MOE_DEC_STAMPS
   unsigned long long* stamps;
 #endif

@@ -87,6 +87,8 @@ _SIGS = {
     "llb_moe_hip_set_q8_gemm": (C.c_int, [C.c_int]),
     "llb_moe_hip_q8_gemm": (C.c_int, []),
     "llb_moe_hip_set_group_scan": (C.c_int, [C.c_int]),
+    "llb_moe_hip_set_lean_topk": (C.c_int, [C.c_int]),
+    "llb_moe_hip_lean_topk": (C.c_int, []),
     "llb_moe_hip_group_scan": (C.c_int, []),
     "llb_moe_hip_group_scratch_bytes": (C.c_size_t, [C.c_uint32, C.c_uint32]),
     "llb_moe_hip_pack_bytes": (C.c_size_t, [C.POINTER(MoeLayer)]),

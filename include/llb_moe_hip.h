@@ -243,6 +243,12 @@ size_t llb_moe_hip_group_scratch_bytes(uint32_t n, uint32_t ne);
  * No counterpart in the reference (llb_mx_group is one fixed kernel). */
 int llb_moe_hip_set_group_scan(int on);
 int llb_moe_hip_group_scan(void);
+/* The one-token decode's routing inside its gate / up launch: off (the default), the 1024-thread top-k
+ * with seven barriers; on, for ne <= 256 and nk <= 16, a variant with four barriers (a key's place in its
+ * 64-expert group and a candidate's rank counted in registers by readlane). Same ids, weights and bits.
+ * Off until the variant has run on a GPU. No counterpart in the reference. */
+int llb_moe_hip_set_lean_topk(int on);
+int llb_moe_hip_lean_topk(void);
 /* pf_q8x (tools/pf27/pfmm.cuh:39-54): n f32 (n % 32 == 0) -> q int8 [n], ds float2 {d, s} [n / 32] */
 int llb_moe_hip_q8_1(llb_dptr x, uint32_t n, llb_dptr q, llb_dptr ds);
 /* rows of a stack dequantized to f32 (the decoders the kernels use; q8g_w / q4k_w / q6k_w / q5k_w) */

@@ -423,6 +423,13 @@ void mo_topk(const float* lg, u32 ne, u32 nk, float sg, u32* ids, float* wt, flo
     for (u32 e = 0; e < ne; e++) {
       if (p[e] > bv) { bv = p[e]; bi = e; } /* strict >: the lower index keeps a tie */
     }
+    if (bi == 0xffffffffu) {
+      /* no p left to take (a NaN or +inf logit makes every p NaN): the reference's slot would hold
+       * 0xffffffff (undefined input); the path keeps expert 0 with p 0 in such a slot, and so does this */
+      ids[j] = 0;
+      wt[j] = 0.0f;
+      continue;
+    }
     ids[j] = bi;
     wt[j] = bv;
     p[bi] = -2.0f;
