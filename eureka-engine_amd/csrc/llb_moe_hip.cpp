@@ -22,6 +22,7 @@ void moe_q8_set_gemm(bool on);
 bool moe_q8_gemm_enabled();
 int launch_q8_1(const float* x, uint32_t n, int8_t* q, float2* ds, hipStream_t st);
 int launch_spin(uint32_t us, hipStream_t st);
+int launch_zero(void* p, uint64_t n, hipStream_t st);
 
 static thread_local char g_err[512];
 static hipStream_t g_stream = nullptr;
@@ -163,7 +164,12 @@ llb_dptr llb_hip_alloc_zero(size_t bytes) {
   return (llb_dptr)(uintptr_t)p;
 }
 int llb_hip_free(llb_dptr p) { return hip_ok(hipFree(dp<void>(p)), "hipFree"); }
-int llb_hip_zero(llb_dptr p, size_t bytes) { return hip_ok(hipMemsetAsync(dp<void>(p), 0, bytes, g_stream), "llb_zero"); }
+// a fill kernel, not hipMemsetAsync: inside a graph capture it is recorded as a kernel node (the
+// reference's CUDA twin leaves its capture instead, host/llb_backend_cuda.h:193-196)
+int llb_hip_zero(llb_dptr p, size_t bytes) {
+  if (bytes && !p) return fail(LLB_HIP_EINVAL, "llb_zero: null buffer");
+  return launched(launch_zero(dp<void>(p), bytes, g_stream), "llb_zero");
+}
 int llb_hip_copy(llb_dptr d, llb_dptr s, size_t bytes) {
   return hip_ok(hipMemcpyAsync(dp<void>(d), dp<void>(s), bytes, hipMemcpyDeviceToDevice, g_stream), "llb_copy");
 }

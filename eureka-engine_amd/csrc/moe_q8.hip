@@ -569,6 +569,26 @@ int moe_q8_forward(const llb_moe_layer* L, uint32_t T, const float* h2, const fl
   return 0;
 }
 
+// ---------------------------------------------------------------- zero fill (llb_zero)
+
+// bytes [p, p + n) to zero by vector stores: the 16-byte-aligned body as uint4, the unaligned head and
+// tail as bytes. A kernel, not a memset, so that a graph capture records a kernel node (memset nodes have
+// given wrong results on replay). Grid-stride over the body, every store inside [p, p + n).
+__global__ void __launch_bounds__(256) k_zero(u8* __restrict__ p, u64 n) {
+  const u64 a = (u64)(uintptr_t)p, b0 = ((a + 15) & ~15ull) - a;  // head bytes before the aligned body
+  const u64 head = b0 < n ? b0 : n, body = (n - head) / 16, tail0 = head + 16 * body;
+  const u64 i0 = (u64)blockIdx.x * 256 + threadIdx.x, step = (u64)gridDim.x * 256;
+  for (u64 i = i0; i < body; i += step) *(uint4*)(p + head + 16 * i) = make_uint4(0u, 0u, 0u, 0u);
+  if (i0 < head) p[i0] = 0;
+  if (i0 < n - tail0) p[tail0 + i0] = 0;
+}
+int launch_zero(void* p, uint64_t n, hipStream_t st) {
+  if (n == 0) return 0;
+  const u64 units = (n + 15) / 16, blocks = (units + 255) / 256;
+  hipLaunchKernelGGL(k_zero, dim3((u32)(blocks < 4096 ? (blocks ? blocks : 1) : 4096)), dim3(256), 0, st, (u8*)p, (u64)n);
+  return 0;
+}
+
 // ---------------------------------------------------------------- a bounded stall (timing aid)
 
 __global__ void k_spin(u64 ticks) {
