@@ -1027,8 +1027,9 @@ static int gu_dec_one(const DecGuArgs& a, hipStream_t st) {
   constexpr u32 RB = rb2048(F), RBS = rb2048(FS);
   constexpr size_t lds = gu_lds(RB > RBS ? RB : RBS);
   static_assert(lds <= 160 * 1024, "LDS of the gate / up block");
-  static bool set = false;
-  if (!set) {
+  static std::atomic<uint64_t> set{0};
+  const uint64_t bit = dev_bit();
+  if (dev_needs_setup(set, bit)) {
     if (hipFuncSetAttribute((const void*)k_gu_dec<F, FS, 4, Q8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
             hipSuccess ||
         hipFuncSetAttribute((const void*)k_gu_dec<F, FS, 8, Q8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
@@ -1038,7 +1039,7 @@ static int gu_dec_one(const DecGuArgs& a, hipStream_t st) {
       (void)hipGetLastError();
       return -1;
     }
-    set = true;
+    set.fetch_or(bit);
   }
   // experts a lane holds in top-k (ne / 64, rounded up to 4, 8 or 16)
   if (a.tk.ne <= 256) LAUNCH_K((k_gu_dec<F, FS, 4, Q8>), dim3(a.nrb), dim3(64 * GU_WAVES), lds, st, a);
@@ -1063,14 +1064,19 @@ int launch_gu_dec(DecGuArgs a, u32 f, u32 fs, bool q8, hipStream_t st) {
 
 template <u32 FD, u32 FS, bool Q8>
 static int dn_dec_one(const DecDnArgs& a, u32 nt, size_t lds, hipStream_t st) {
-  static size_t set = 0;  // the dynamic LDS the kernel is allowed so far
-  if (lds > set) {
+  static std::atomic<size_t> set[64];  // per device: the dynamic LDS the kernel is allowed so far
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+    (void)hipGetLastError();
+    dev = 0;
+  }
+  if (dev >= 64 || lds > set[dev].load()) {
     if (hipFuncSetAttribute((const void*)k_dn_dec<FD, FS, Q8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
         hipSuccess) {
       (void)hipGetLastError();
       return -1;
     }
-    set = lds;
+    if (dev < 64) set[dev].store(lds);
   }
   LAUNCH_K((k_dn_dec<FD, FS, Q8>), dim3((a.dm + DN_RB - 1) / DN_RB), dim3(64 * nt), lds, st, a);
   return 0;

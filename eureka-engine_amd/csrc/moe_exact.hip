@@ -1201,13 +1201,14 @@ int launch_tree_rows(const TreeArgs& a, u32 nsp, hipStream_t st) {
       if (cost < best) { best = cost; ntb = n; }
     }
     const dim3 grid(rb, (nt + ntb - 1) / ntb);
-    static bool set = false;
-    if (!set) {
+    static std::atomic<uint64_t> set{0};
+    const uint64_t bit = dev_bit();
+    if (dev_needs_setup(set, bit)) {
       (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<1, 4, 4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(4 * 64 * 36 * 4));
       (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<1, 4, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(4 * 64 * 36 * 4));
       (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<2, 4, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(4 * 64 * 68 * 4));
       (void)hipFuncSetAttribute((const void*)k_tree_rows_mt<2, 4, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(4 * 64 * 68 * 4));
-      set = true;
+      set.fetch_or(bit);
     }
     if (nsp == 1 && rw == 4) LAUNCH_K((k_tree_rows_mt<1, 4, 4>), grid, dim3(256), sm, st, a, ntb);
     else if (nsp == 1) LAUNCH_K((k_tree_rows_mt<1, 4, 1>), grid, dim3(256), sm, st, a, ntb);

@@ -778,10 +778,11 @@ int launch_gemm_i8(const GemmQ8Args& g, u32 fm, u32 mode, u32 grid_y, hipStream_
 // ---------------------------------------------------------------- launchers
 
 template <u32 F, u32 MODE, bool PKD> static void gemm3_go(const GemmArgs& g, dim3 grid, size_t sm, hipStream_t st) {
-  static bool set = false;
-  if (!set) {
+  static std::atomic<uint64_t> set{0};
+  const uint64_t bit = dev_bit();
+  if (dev_needs_setup(set, bit)) {
     (void)hipFuncSetAttribute((const void*)k_moe_gemm3<F, MODE, PKD>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
-    set = true;
+    set.fetch_or(bit);
   }
   LAUNCH_K((k_moe_gemm3<F, MODE, PKD>), grid, dim3(256), sm, st, g, g.N / (MODE == 0 ? 128u : 256u));
 }

@@ -19,6 +19,19 @@ bool stage_armed(hipEvent_t* a, hipEvent_t* b);
 void stage_begin(int s);
 void stage_end(int s);
 
+// Kernel attributes (the dynamic-LDS limit) are per device: a launch site keeps a mask of the devices
+// it has set them on. dev_bit() is the current device's bit (devices past 63: 0, set up every time).
+#include <atomic>
+inline uint64_t dev_bit() {
+  int d = 0;
+  if (hipGetDevice(&d) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return d >= 0 && d < 64 ? 1ull << d : 0;
+}
+inline bool dev_needs_setup(const std::atomic<uint64_t>& mask, uint64_t bit) { return !bit || !(mask.load() & bit); }
+
 struct TreeSeg {
   const uint8_t* W;  // rows of `cols` columns
   uint32_t fm;
